@@ -1,0 +1,197 @@
+"""Benchmark: fused attention forward + backward on one MI355X.
+
+Workload (the headline config): n_embed=1280,
+n_head=10, n_kv_head=5, head_dim=128, T=2048, B=16, bf16 fast mode, full
+causal window, RMS-normalised Q/K, V ~ N(0,1), dO ~ N(0,0.1), synthetic data.
+A step is one forward (O, l, m) plus one backward (dQ, dK, dV, overwrite)
+over the whole batch, with every input resident in HBM.
+
+value = algorithmic TFLOP/s = 14 * D * visible_pairs / step time (the
+FlashAttention convention: fwd 4*D, bwd 10*D per visible (q,k) pair).
+The per-kernel durations come from HIP events the library records around
+each of its launches on the launch stream during the timed steps.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA, published
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
+
+METRIC = "attention fwd+bwd TFLOP/s and % MFMA peak on 1 MI355X; vs Julia CPU ref"
+
+
+def kernel_flops(name: str, D: int, pairs: int, B: int, T: int, H: int) -> tuple:
+    """(bound, algorithmic amount per launch, unit) of one library kernel.
+
+    fwd: the two products S=QK^T and O=PV, 4*D per visible pair.
+    dkdv: the four products S, dP, dV, dK, 8*D per pair.
+    dq: the dQ product only, 2*D per pair (its S/dP recomputation is overhead).
+    pre: HBM bytes: read dO, O (bf16), l, m; write Delta, lse2 (fp32).
+    """
+    if name.startswith("attn_fwd"):
+        return "mfma", 4 * D * pairs, "flop"
+    if name.startswith("attn_bwd_dkdv"):
+        return "mfma", 8 * D * pairs, "flop"
+    if name.startswith("attn_bwd_dq"):
+        return "mfma", 2 * D * pairs, "flop"
+    if name.startswith("attn_bwd_pre"):
+        return "hbm", B * T * H * (2 * D * 2 + 4 * 4), "byte"
+    return "hbm", 0, "byte"
+
+
+def cpu_baseline(wl, rows: int, threads: int) -> dict:
+    """Time the reference's blocked FA-1 CPU algorithm (float32 restatement in
+    oracle/fa1.c, 512-blocks, no skipping) on a bounded sample of the same
+    workload: ``rows`` batch rows, all heads, bf16 inputs upcast to fp32."""
+    import numpy as np
+
+    from femtochat_amd import workloads as W
+    from oracle import fa1
+
+    h = W.host_inputs(wl, 0, batch=list(range(rows)))
+    fa1.forward(h.Q[:, :64], h.K[:, :64], h.V[:, :64], h.window, nthreads=threads)  # warm-up (loads, pages)
+    t0 = time.perf_counter()
+    O, l, m = fa1.forward(h.Q, h.K, h.V, h.window, h.positions, nthreads=threads)
+    t1 = time.perf_counter()
+    fa1.backward(h.dO, h.Q, h.K, h.V, O, l, m, h.window, h.positions, nthreads=threads)
+    t2 = time.perf_counter()
+    pairs = W.visible_pairs(wl.T, rows, wl.H, h.window, h.positions)
+    flop = 14 * wl.D * pairs
+    assert np.isfinite(O).all()
+    return {
+        "value": flop / (t2 - t0) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{wl.name} batch rows 0..{rows - 1} of {wl.B}, all {wl.H} heads, T={wl.T}: fwd {t1 - t0:.2f} s "
+                   f"+ bwd {t2 - t1:.2f} s; float32 restatement of flash_attention₁!/Δflash_attention₁! "
+                   "(src/kernels.jl:131-379, 512-blocks, no tile skipping) on bf16-rounded inputs upcast to fp32; "
+                   "TFLOP/s counts algorithmic visible-pair FLOPs like the GPU value"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="C3")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=2)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box in this build has a single MI355X, and the attention "
+              f"kernels need no collective (--gpus {args.gpus} is not supported).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import femtochat_amd._lib as L
+    from femtochat_amd import MFMAExact, MFMAFast, attention_, backward_workspace_bytes, delta_attention_
+    from femtochat_amd import workloads as W
+
+    wl = W.WORKLOADS[args.workload]
+    dev = torch.device("cuda", 0)
+    fast = wl.mode == "fast"
+    A = MFMAFast() if fast else MFMAExact()
+    dt = torch.bfloat16 if fast else torch.float32
+
+    layers = []
+    total_pairs = 0
+    for layer in range(wl.layers):
+        Q, K, V, dO, pos, window = W.device_inputs(wl, layer, dev)
+        O = torch.empty_like(Q)
+        l = torch.empty((wl.B, wl.H, wl.T), device=dev)
+        m = torch.empty((wl.B, wl.H, wl.T), device=dev)
+        dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+        ws = torch.empty(backward_workspace_bytes(A, Q, K, positions=pos), dtype=torch.uint8, device=dev)
+        pairs = W.visible_pairs(wl.T, wl.B, wl.H, window, None if pos is None else pos.cpu().numpy())
+        total_pairs += pairs
+        layers.append((Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws, pairs))
+
+    def step():
+        for (Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws, _) in layers:
+            attention_(A, O, l, m, Q, K, V, window, positions=pos)
+            delta_attention_(A, dQ, dK, dV, dO, Q, K, V, O, l, m, window, positions=pos, accumulate=False,
+                             workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    L.profile_collect()  # discard anything recorded before
+    L.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.profile_enable(False)
+    kernels = L.profile_collect()
+
+    ms = (t1 - t0) * 1e3 / args.steps
+    flop = 14 * wl.D * total_pairs
+    value = flop / (ms * 1e-3) / 1e12
+    peak = PEAK_BF16_TFLOPS if fast else PEAK_FP32_TFLOPS
+
+    per_kernel = {}
+    for name, (n, tot) in sorted(kernels.items()):
+        avg = tot / n
+        bound, amount, unit = kernel_flops(name, wl.D, total_pairs // wl.layers, wl.B, wl.T, wl.H)
+        rate = amount / (avg * 1e-3)
+        per_kernel[name] = {"launches": n, "avg_ms": round(avg, 4), "bound": bound,
+                            "achieved": round(rate / (1e12 if unit == "flop" else 1e9), 2),
+                            "unit": "TFLOP/s" if unit == "flop" else "GB/s"}
+    dominant = max(kernels.items(), key=lambda kv: kv[1][1])[0]
+    dk = per_kernel[dominant]
+    dpeak = peak if dk["bound"] == "mfma" else PEAK_HBM_GBS
+    roofline = {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dpeak,
+                "unit": dk["unit"], "frac": round(dk["achieved"] / dpeak, 4), "traffic": None}
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(wl, min(args.cpu_rows, wl.B), threads)
+        cpu["value"] = round(cpu["value"], 5)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if fast else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{wl.name}: {wl.description}",
+            "D": wl.D, "H": wl.H, "Hkv": wl.Hkv, "T": wl.T, "B": wl.B, "windows": [list(w) for w in wl.windows],
+            "mode": wl.mode, "visible_pairs": total_pairs, "flop_per_step": flop,
+            "mfma_peak_frac": round(value / peak, 4), "peak_tflops": peak,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": per_kernel,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,24 @@
+"""MI355X-native flash attention for femtochat (forward and backward).
+
+The compute path is libfemtochat_attn.so (hand-written gfx950 HIP kernels
+behind a C ABI, include/femtochat_attn.h); ``femtochat_amd.kernels`` is the
+host-side mirror of the reference's ``Kernels`` attention API.
+"""
+from .kernels import (  # noqa: F401
+    AttentionFunction,
+    AttentionState,
+    MFMAExact,
+    MFMAFast,
+    accumulator_type,
+    attention,
+    attention_,
+    attention_inputs,
+    attention_state,
+    backward_workspace_bytes,
+    capabilities,
+    delta_attention_,
+    instruction,
+    window_sizes,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,328 @@
+// C ABI of libfemtochat_attn.so: host-side validation, workspace sizing and
+// dispatch to the gfx950 kernels.  Declarations and semantics are in
+// include/femtochat_attn.h.
+//
+// Error handling mirrors the reference's rule that no exception crosses the
+// foreign boundary (ext/reactant/cuda_call.jl:45-48): every failure becomes an
+// fc_status plus a thread-local message.
+#include "../../include/femtochat_attn.h"
+#include "attn_launch.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+fc_status fail(fc_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+fc_status fail(fc_status code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+fc_status ok() {
+  g_last_error.clear();
+  return FC_OK;
+}
+
+bool valid_dtype(int32_t d) { return d == FC_F32 || d == FC_BF16; }
+
+// Validates the descriptor and fills the normalised problem.
+fc_status make_problem(const fc_attn_desc* d, fc::Problem* p) {
+  if (d == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "descriptor is null");
+  if (d->D <= 0 || d->H <= 0 || d->Hkv <= 0 || d->T <= 0 || d->B <= 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "sizes must be positive (D=%d H=%d Hkv=%d T=%d B=%d)", d->D, d->H,
+                d->Hkv, d->T, d->B);
+  if (d->H % d->Hkv != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "n_head %d is not a multiple of n_kv_head %d", d->H, d->Hkv);
+  if (d->D % 16 != 0 || d->D > 128)
+    return fail(FC_ERR_INVALID_ARGUMENT, "head_dim %d must be a multiple of 16 and at most 128", d->D);
+  if (!fc::head_dim_supported(d->D))
+    return fail(FC_ERR_UNSUPPORTED, "head_dim %d is not compiled in (supported: 16, 32, 64, 128)", d->D);
+  const int64_t rows = (int64_t)d->B * d->T * d->H;
+  if (rows * d->D >= (int64_t)1 << 40 || (int64_t)d->T * d->H * d->B > INT32_MAX / 2)
+    return fail(FC_ERR_UNSUPPORTED, "problem too large");
+  if (!valid_dtype(d->in_dtype) || !valid_dtype(d->out_dtype) || !valid_dtype(d->dout_dtype) ||
+      !valid_dtype(d->grad_dtype))
+    return fail(FC_ERR_INVALID_ARGUMENT, "dtype codes must be FC_F32 or FC_BF16");
+  if (d->mode == FC_MODE_EXACT) {
+    if (d->in_dtype != FC_F32 || d->out_dtype != FC_F32 || d->dout_dtype != FC_F32 || d->grad_dtype != FC_F32)
+      return fail(FC_ERR_INVALID_ARGUMENT, "exact mode takes and returns float32 only");
+  } else if (d->mode == FC_MODE_FAST) {
+    if (d->in_dtype != FC_BF16)
+      return fail(FC_ERR_INVALID_ARGUMENT, "fast mode takes bfloat16 Q/K/V (convert first, as attention_inputs does)");
+  } else {
+    return fail(FC_ERR_INVALID_ARGUMENT, "unknown mode %d", d->mode);
+  }
+  if ((d->flags & ~FC_FLAG_OVERWRITE) != 0) return fail(FC_ERR_INVALID_ARGUMENT, "unknown flag bits 0x%x", d->flags);
+
+  p->D = d->D;
+  p->H = d->H;
+  p->Hkv = d->Hkv;
+  p->T = d->T;
+  p->B = d->B;
+  p->group = d->H / d->Hkv;
+  int64_t left = d->win_left, right = d->win_right;
+  if (left == -1 && right == 0) left = d->T;  // causal sentinel (src/kernels.jl:35-36)
+  // Clamping to [-T-1, T] keeps q - left and q + right in range without
+  // changing which keys of [0, T) are visible.
+  const int64_t lo = -(int64_t)d->T - 1, hi = d->T;
+  p->left = (int)std::min(std::max(left, lo), hi);
+  p->right = (int)std::min(std::max(right, lo), hi);
+  p->bf16 = d->mode == FC_MODE_FAST;
+  p->out_bf16 = d->out_dtype == FC_BF16;
+  p->dout_bf16 = d->dout_dtype == FC_BF16;
+  p->grad_bf16 = d->grad_dtype == FC_BF16;
+  p->accumulate = (d->flags & FC_FLAG_OVERWRITE) == 0;
+  p->positions = false;
+  return FC_OK;
+}
+
+// ---- profiling --------------------------------------------------------------
+struct Record {
+  hipEvent_t begin, end;
+  std::string kernel;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<Record> g_records;
+
+}  // namespace
+
+namespace fc {
+
+ProfileMark profile_begin(hipStream_t s) {
+  ProfileMark mk;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (!g_prof_on) return mk;
+  }
+  hipEvent_t ev;
+  if (hipEventCreate(&ev) != hipSuccess) return mk;
+  (void)hipEventRecord(ev, s);
+  mk.begin = ev;
+  return mk;
+}
+
+void profile_end(const ProfileMark& mark, const char* kernel, hipStream_t s) {
+  if (mark.begin == nullptr) return;
+  hipEvent_t ev;
+  if (hipEventCreate(&ev) != hipSuccess) {
+    (void)hipEventDestroy(static_cast<hipEvent_t>(mark.begin));
+    return;
+  }
+  (void)hipEventRecord(ev, s);
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_records.push_back(Record{static_cast<hipEvent_t>(mark.begin), ev, kernel});
+}
+
+}  // namespace fc
+
+extern "C" {
+
+int32_t fc_abi_version(void) { return FC_ATTN_ABI_VERSION; }
+
+const char* fc_last_error(void) { return g_last_error.c_str(); }
+
+uint32_t fc_attn_supported_head_dims(void) {
+  uint32_t mask = 0;
+  for (int D = 16; D <= 128; D += 16)
+    if (fc::head_dim_supported(D)) mask |= 1u << (D / 16 - 1);
+  return mask;
+}
+
+fc_status fc_attn_workspace_bytes(const fc_attn_desc* desc, int32_t pass, int32_t positions_given, size_t* bytes) {
+  fc::Problem p;
+  const fc_status st = make_problem(desc, &p);
+  if (st != FC_OK) return st;
+  if (bytes == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "bytes is null");
+  p.positions = positions_given != 0;
+  if (pass == FC_PASS_FORWARD) {
+    *bytes = 0;
+  } else if (pass == FC_PASS_BACKWARD) {
+    *bytes = fc::bwd_workspace(p).total;
+  } else {
+    return fail(FC_ERR_INVALID_ARGUMENT, "unknown pass %d", pass);
+  }
+  return ok();
+}
+
+fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, const void* V,
+                      const int32_t* positions, void* O, float* l, float* m, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  fc::Problem p;
+  fc_status st = make_problem(desc, &p);
+  if (st != FC_OK) return st;
+  if (Q == nullptr || K == nullptr || V == nullptr || O == nullptr || l == nullptr || m == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_attn_fwd: a required pointer is null");
+  p.positions = positions != nullptr;
+  fc::FwdArgs a{};
+  a.Q = Q;
+  a.K = K;
+  a.V = V;
+  a.pos = positions;
+  a.O = O;
+  a.l = l;
+  a.m = m;
+  a.H = p.H;
+  a.Hkv = p.Hkv;
+  a.T = p.T;
+  a.B = p.B;
+  a.group = p.group;
+  a.left = p.left;
+  a.right = p.right;
+  a.out_bf16 = p.out_bf16 ? 1 : 0;
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)p.D));
+  const hipError_t e = fc::launch_fwd(p, a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, const void* K, const void* V,
+                      const void* O, const float* l, const float* m, const int32_t* positions, void* dQ,
+                      void* dK, void* dV, void* workspace, size_t workspace_bytes, void* stream) {
+  fc::Problem p;
+  fc_status st = make_problem(desc, &p);
+  if (st != FC_OK) return st;
+  if (dO == nullptr || Q == nullptr || K == nullptr || V == nullptr || O == nullptr || l == nullptr ||
+      m == nullptr || dQ == nullptr || dK == nullptr || dV == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_attn_bwd: a required pointer is null");
+  p.positions = positions != nullptr;
+  const fc::BwdWorkspace ws = fc::bwd_workspace(p);
+  if (workspace == nullptr || workspace_bytes < ws.total)
+    return fail(FC_ERR_WORKSPACE, "backward workspace needs %zu bytes, got %zu%s", ws.total, workspace_bytes,
+                workspace == nullptr ? " (null)" : "");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(FC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char* w = static_cast<char*>(workspace);
+
+  fc::PreArgs pa{};
+  pa.dO = dO;
+  pa.O = O;
+  pa.l = l;
+  pa.m = m;
+  pa.delta = reinterpret_cast<float*>(w + ws.delta);
+  pa.lse2 = reinterpret_cast<float*>(w + ws.lse2);
+  pa.dO16 = (p.bf16 && !p.dout_bf16) ? w + ws.dO16 : nullptr;
+  pa.H = p.H;
+  pa.T = p.T;
+  pa.B = p.B;
+  pa.dO_bf16 = p.dout_bf16 ? 1 : 0;
+  pa.O_bf16 = p.out_bf16 ? 1 : 0;
+  hipError_t e = fc::launch_bwd_pre(p, pa, s);
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "backward preprocess launch failed: %s", hipGetErrorString(e));
+
+  int32_t* chunk_lb = nullptr;
+  if (p.positions) {
+    chunk_lb = reinterpret_cast<int32_t*>(w + ws.chunk_lb);
+    fc::BoundsArgs ba{positions, chunk_lb, p.T, p.B, p.left};
+    e = fc::launch_bounds(p, ba, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "bounds launch failed: %s", hipGetErrorString(e));
+  }
+
+  fc::BwdArgs a{};
+  a.dO = pa.dO16 != nullptr ? pa.dO16 : dO;
+  a.Q = Q;
+  a.K = K;
+  a.V = V;
+  a.delta = pa.delta;
+  a.lse2 = pa.lse2;
+  a.pos = positions;
+  a.chunk_lb = chunk_lb;
+  a.dQ = dQ;
+  a.dK = dK;
+  a.dV = dV;
+  a.H = p.H;
+  a.Hkv = p.Hkv;
+  a.T = p.T;
+  a.B = p.B;
+  a.group = p.group;
+  a.left = p.left;
+  a.right = p.right;
+  a.grad_bf16 = p.grad_bf16 ? 1 : 0;
+  a.accumulate = p.accumulate ? 1 : 0;
+  a.scale = (float)(1.0 / std::sqrt((double)p.D));
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)p.D));
+  e = fc::launch_bwd_dkdv(p, a, s);
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "dK/dV launch failed: %s", hipGetErrorString(e));
+  e = fc::launch_bwd_dq(p, a, s);
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "dQ launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+fc_status fc_capabilities(int32_t device, fc_caps* caps) {
+  if (caps == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "caps is null");
+  hipDeviceProp_t prop;
+  const hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  std::memset(caps, 0, sizeof(*caps));
+  std::snprintf(caps->name, sizeof(caps->name), "%s", prop.name);
+  std::snprintf(caps->arch, sizeof(caps->arch), "%s", prop.gcnArchName);
+  caps->compute_units = prop.multiProcessorCount;
+  caps->wavefront_size = prop.warpSize;
+  caps->lds_bytes_per_block = (int32_t)prop.sharedMemPerBlock;
+  caps->max_threads_per_block = prop.maxThreadsPerBlock;
+  caps->clock_khz = prop.clockRate;
+  caps->global_mem_bytes = (int64_t)prop.totalGlobalMem;
+  return ok();
+}
+
+fc_status fc_profile_enable(int32_t enable) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_on = enable != 0;
+  return ok();
+}
+
+fc_status fc_profile_collect(fc_kernel_time* out, int32_t capacity, int32_t* count) {
+  std::vector<Record> recs;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    recs.swap(g_records);
+  }
+  std::map<std::string, std::pair<int32_t, double>> agg;
+  hipError_t err = hipSuccess;
+  for (const Record& r : recs) {
+    float ms = 0.0f;
+    hipError_t e = hipEventSynchronize(r.end);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.begin, r.end);
+    if (e != hipSuccess && err == hipSuccess) err = e;
+    auto& slot = agg[r.kernel];
+    slot.first += 1;
+    slot.second += ms;
+    (void)hipEventDestroy(r.begin);
+    (void)hipEventDestroy(r.end);
+  }
+  if (err != hipSuccess) return fail(FC_ERR_HIP, "profile events: %s", hipGetErrorString(err));
+  int32_t n = 0;
+  for (const auto& kv : agg) {
+    if (out != nullptr && n < capacity) {
+      std::memset(&out[n], 0, sizeof(out[n]));
+      std::snprintf(out[n].kernel, sizeof(out[n].kernel), "%s", kv.first.c_str());
+      out[n].launches = kv.second.first;
+      out[n].total_ms = kv.second.second;
+    }
+    ++n;
+  }
+  if (count != nullptr) *count = n;
+  return ok();
+}
+
+}  // extern "C"

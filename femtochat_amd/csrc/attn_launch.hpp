@@ -1,0 +1,95 @@
+// Internal interface between the C ABI (attn_api.hip) and the kernels
+// (attn_fwd.hip, attn_bwd.hip).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fc {
+
+// Normalised problem: window already mapped to (left,right) with the causal
+// sentinel (-1,0) replaced by (T,0) and both extents clamped to [-T-1, T].
+struct Problem {
+  int D, H, Hkv, T, B, group;
+  int left, right;
+  bool bf16;        // fast mode (bf16 inputs) vs exact mode (fp32)
+  bool out_bf16;    // O storage
+  bool dout_bf16;   // dO storage
+  bool grad_bf16;   // dQ/dK/dV storage
+  bool accumulate;  // backward adds into dQ/dK/dV
+  bool positions;
+};
+
+struct FwdArgs {
+  const void* Q;
+  const void* K;
+  const void* V;
+  const int32_t* pos;
+  void* O;
+  float* l;
+  float* m;
+  int H, Hkv, T, B, group, left, right;
+  int out_bf16;
+  float scale_log2;
+};
+
+struct PreArgs {
+  const void* dO;
+  const void* O;
+  const float* l;
+  const float* m;
+  float* delta;
+  float* lse2;
+  void* dO16;  // bf16 copy of an fp32 dO (fast mode only), else null
+  int H, T, B;
+  int dO_bf16, O_bf16;
+};
+
+struct BoundsArgs {
+  const int32_t* pos;
+  int32_t* chunk_lb;  // [B][ceil(T/32)][2] = (min, max) of key_lb
+  int T, B, left;
+};
+
+struct BwdArgs {
+  const void* dO;  // in the input element type (bf16 copy when needed)
+  const void* Q;
+  const void* K;
+  const void* V;
+  const float* delta;
+  const float* lse2;
+  const int32_t* pos;
+  const int32_t* chunk_lb;
+  void* dQ;
+  void* dK;
+  void* dV;
+  int H, Hkv, T, B, group, left, right;
+  int grad_bf16, accumulate;
+  float scale;       // 1/sqrt(D)
+  float scale_log2;  // log2(e)/sqrt(D)
+};
+
+// Workspace layout of the backward pass (byte offsets, 256-aligned).
+struct BwdWorkspace {
+  size_t delta, lse2, chunk_lb, dO16, total;
+};
+BwdWorkspace bwd_workspace(const Problem& p);
+
+bool head_dim_supported(int D);
+
+// Kernel launchers (return the hipError_t of the launch).
+hipError_t launch_fwd(const Problem& p, const FwdArgs& a, hipStream_t s);
+hipError_t launch_bwd_pre(const Problem& p, const PreArgs& a, hipStream_t s);
+hipError_t launch_bounds(const Problem& p, const BoundsArgs& a, hipStream_t s);
+hipError_t launch_bwd_dkdv(const Problem& p, const BwdArgs& a, hipStream_t s);
+hipError_t launch_bwd_dq(const Problem& p, const BwdArgs& a, hipStream_t s);
+
+// Profiling hooks (attn_api.hip): bracket one launch with events when enabled.
+struct ProfileMark {
+  void* begin = nullptr;
+};
+ProfileMark profile_begin(hipStream_t s);
+void profile_end(const ProfileMark& mark, const char* kernel, hipStream_t s);
+
+}  // namespace fc

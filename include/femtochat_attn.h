@@ -1,0 +1,149 @@
+/*
+ * femtochat_attn.h — C ABI of the MI355X (gfx950) flash-attention library
+ * libfemtochat_attn.so.
+ *
+ * The library is the device backend for femtochat's attention plug-in API
+ * (`Kernels.attention / attention! / Δattention! / attention_state`,
+ * reference src/kernels.jl:417-433).  A host binding (the Python module
+ * femtochat_amd.kernels, or a Julia `ccall` extension) owns every buffer and
+ * passes raw device pointers; the library validates the descriptor on the
+ * host, then launches its HIP kernels asynchronously on the caller's stream.
+ *
+ * Tensor layout is the reference's column-major layout, written here as C
+ * row-major index expressions (0-based):
+ *   Q, O, dO, dQ  (D,H,T,B)   : X[((b*T + t)*H   + h)*D + d]
+ *   K, V, dK, dV  (D,Hkv,T,B) : X[((b*T + t)*Hkv + h)*D + d]
+ *   l, m          (1,T,H,B)   : x[(b*H + h)*T + t]            (float32)
+ *   positions     (T,B) Int32 : p[b*T + t]
+ *
+ * Semantics (reference src/kernels.jl:30-42, 131-219, 287-379):
+ *   key k is visible to query q iff  q-left <= k <= q+right, and k <= q when
+ *   (left,right) == (-1,0) (the causal sentinel).  With positions, a key must
+ *   also satisfy k >= q - positions[q] (it lies in the query's document).
+ *   m = max over visible keys of S/sqrt(D) (natural-log units);
+ *   l = sum over visible keys of exp(S/sqrt(D) - m);  O = sum P V.
+ *   A query with no visible key gets O = 0, l = 0, m = -FLT_MAX.
+ *   GQA: query head h (0-based) reads KV head h / (H/Hkv).
+ *   The backward ADDS into dQ/dK/dV unless FC_FLAG_OVERWRITE is set
+ *   (reference src/kernels.jl:358,371,374; ext/FemtoChatCUDAExt.jl:1756-1760).
+ *
+ * Errors: every entry point returns an fc_status; nothing is thrown across
+ * the ABI.  fc_last_error() gives the calling thread's last message.
+ * Threading: reentrant; launches are asynchronous on the given stream; no
+ * entry point synchronises the device or allocates device memory.
+ */
+#ifndef FEMTOCHAT_ATTN_H
+#define FEMTOCHAT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FC_ATTN_ABI_VERSION 1
+
+typedef enum {
+  FC_OK = 0,
+  FC_ERR_INVALID_ARGUMENT = 1, /* bad shape, window, dtype, null pointer */
+  FC_ERR_UNSUPPORTED = 2,      /* valid but not implemented (e.g. head_dim) */
+  FC_ERR_WORKSPACE = 3,        /* workspace missing or too small */
+  FC_ERR_HIP = 4               /* a HIP runtime call failed */
+} fc_status;
+
+typedef enum { FC_F32 = 0, FC_BF16 = 1 } fc_dtype;
+
+typedef enum {
+  /* fp32 in, fp32 MFMA, fp32 out (analogue of SIMTInstruction,
+     reference ext/FemtoChatCUDAExt.jl:243-1002) */
+  FC_MODE_EXACT = 0,
+  /* bf16 Q/K/V/dO, bf16 MFMA with fp32 accumulation and statistics; P and dS
+     rounded to bf16 before their second product (analogue of
+     TensorCoreInstruction, reference ext/FemtoChatCUDAExt.jl:1004-2068) */
+  FC_MODE_FAST = 1
+} fc_mode;
+
+/* fc_attn_desc.flags */
+#define FC_FLAG_OVERWRITE 1u /* backward writes dQ/dK/dV instead of adding */
+
+typedef struct {
+  int32_t D, H, Hkv, T, B;      /* head_dim, query heads, KV heads, tokens, batch */
+  int32_t win_left, win_right;  /* window (left,right); (-1,0) = causal */
+  int32_t mode;                 /* fc_mode */
+  int32_t in_dtype;             /* Q, K, V  (EXACT: F32; FAST: BF16) */
+  int32_t out_dtype;            /* O        (EXACT: F32; FAST: BF16 or F32) */
+  int32_t dout_dtype;           /* dO       (EXACT: F32; FAST: BF16 or F32) */
+  int32_t grad_dtype;           /* dQ,dK,dV (EXACT: F32; FAST: BF16 or F32) */
+  uint32_t flags;               /* FC_FLAG_* */
+} fc_attn_desc;
+
+typedef enum { FC_PASS_FORWARD = 0, FC_PASS_BACKWARD = 1 } fc_pass;
+
+/* Workspace bytes the given pass needs (0 is possible).  positions_given
+   selects the document-mask variant.  Mirrors the scratch the reference
+   allocates per call (ext/FemtoChatCUDAExt.jl:1797-1801), here caller-owned. */
+fc_status fc_attn_workspace_bytes(const fc_attn_desc* desc, int32_t pass,
+                                  int32_t positions_given, size_t* bytes);
+
+/* Forward: writes O, l, m.  Replaces
+   `attention!(𝒜, O, ℓ, m, Q, K, V, window)` (reference src/kernels.jl:419,
+   CPU body :131-219; CUDA ext/FemtoChatCUDAExt.jl:1242-1260).
+   positions may be NULL (reference semantics, no document mask). */
+fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K,
+                      const void* V, const int32_t* positions, void* O,
+                      float* l, float* m, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Backward: adds (or, with FC_FLAG_OVERWRITE, writes) dQ, dK, dV.  Replaces
+   `Δattention!(𝒜, dQ, dK, dV, dO, Q, K, V, O, ℓ, m, window)` (reference
+   src/kernels.jl:420, CPU body :287-379; CUDA ext/FemtoChatCUDAExt.jl:1771-1790). */
+fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q,
+                      const void* K, const void* V, const void* O,
+                      const float* l, const float* m, const int32_t* positions,
+                      void* dQ, void* dK, void* dV, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Last error message of the calling thread ("" if none). */
+const char* fc_last_error(void);
+
+/* Device introspection, the analogue of `capabilities()`
+   (reference ext/FemtoChatCUDAExt.jl:177-208). */
+typedef struct {
+  char name[64];
+  char arch[32];            /* e.g. "gfx950" */
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int32_t lds_bytes_per_block;
+  int32_t max_threads_per_block;
+  int32_t clock_khz;
+  int64_t global_mem_bytes;
+} fc_caps;
+fc_status fc_capabilities(int32_t device, fc_caps* caps);
+
+/* Supported head dims are reported as a bitmask: bit (D/16 - 1) set when
+   head_dim D is compiled in. */
+uint32_t fc_attn_supported_head_dims(void);
+
+int32_t fc_abi_version(void);
+
+/* Kernel timing for measurement harnesses.  While enabled, every kernel the
+   library launches is bracketed by HIP events on its stream (no host sync).
+   fc_profile_collect synchronises on those events and returns, per kernel
+   name, the launch count and total milliseconds; it then clears the records.
+   No counterpart in the reference (its driver times whole steps,
+   scripts/train.jl:136-175). */
+typedef struct {
+  char kernel[48];
+  int32_t launches;
+  double total_ms;
+} fc_kernel_time;
+fc_status fc_profile_enable(int32_t enable);
+fc_status fc_profile_collect(fc_kernel_time* out, int32_t capacity,
+                             int32_t* count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FEMTOCHAT_ATTN_H */

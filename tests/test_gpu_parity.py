@@ -1,0 +1,285 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the float64 oracle.
+
+Small cases cover every code path (head dims, GQA ratios, ragged T, windows
+including empty rows, document masks, both modes, bf16/fp32 storage); the
+full-size BASELINE workloads C1..C5 are checked on a subset of (batch, KV
+group) slices against the oracle and through size-independent properties.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from femtochat_amd import MFMAExact, MFMAFast
+from femtochat_amd import workloads as W
+from oracle import attention_ref as R
+from tests.helpers import TOL, TOL_LSE, gpu_backward, gpu_forward, lse_err, rel_err, say, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(seed, B, T, H, Hkv, D, fast, rms=True, dO_std=0.1):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    Q = rng.standard_normal((B, T, H, D), dtype=np.float32)
+    K = rng.standard_normal((B, T, Hkv, D), dtype=np.float32)
+    V = rng.standard_normal((B, T, Hkv, D), dtype=np.float32)
+    dO = (rng.standard_normal((B, T, H, D), dtype=np.float32) * dO_std).astype(np.float32)
+    if rms:
+        Q = Q / np.sqrt((Q.astype(np.float64) ** 2).mean(-1, keepdims=True)).astype(np.float32)
+        K = K / np.sqrt((K.astype(np.float64) ** 2).mean(-1, keepdims=True)).astype(np.float32)
+    if fast:
+        Q, K, V, dO = (torch.from_numpy(x).bfloat16().float().numpy() for x in (Q, K, V, dO))
+    return Q, K, V, dO
+
+
+def _dev(x, fast, device):
+    return torch.from_numpy(x).to(device=device, dtype=torch.bfloat16 if fast else torch.float32).contiguous()
+
+
+def _check_case(device, mode, B, T, H, Hkv, D, window, positions=None, seed=0, out_dtype=None, grad_dtype=None,
+                dout_dtype=None):
+    fast = mode == "fast"
+    A = MFMAFast() if fast else MFMAExact()
+    say(f"case mode={mode} B={B} T={T} H={H} Hkv={Hkv} D={D} window={window} pos={positions is not None} "
+        f"out={out_dtype} grad={grad_dtype} dO={dout_dtype}")
+    Q, K, V, dO = _inputs(seed, B, T, H, Hkv, D, fast)
+    Qd, Kd, Vd = (_dev(x, fast, device) for x in (Q, K, V))
+    pos_d = None if positions is None else torch.from_numpy(positions).to(device).contiguous()
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, window, pos_d, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    O_ref, l_ref, m_ref = R.forward(Q, K, V, window, positions)
+    tol = TOL[mode]
+    eO = rel_err(to_np(O), O_ref)
+    eL = lse_err(to_np(l), to_np(m), l_ref, m_ref)
+    empty = l_ref == 0
+    assert eO <= tol, f"O rel err {eO}"
+    assert eL <= TOL_LSE, f"LSE err {eL}"
+    assert np.all(to_np(l)[empty] == 0) and np.all(to_np(m)[empty] == -R.FLT_MAX), "empty rows must give l=0, m=-floatmax"
+    assert np.all(to_np(O)[np.transpose(empty, (0, 2, 1))] == 0), "empty rows must give O=0"
+
+    # Backward with the GPU's own saved state on both sides.
+    dOd = torch.from_numpy(dO).to(device=device, dtype=(dout_dtype or (torch.bfloat16 if fast else torch.float32)))
+    dQ, dK, dV = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, window, pos_d, grad_dtype=grad_dtype)
+    torch.cuda.synchronize()
+    g_ref = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), window, positions)
+    for name, x, r in zip(("dQ", "dK", "dV"), (dQ, dK, dV), g_ref):
+        e = rel_err(to_np(x), r)
+        assert e <= tol, f"{name} rel err {e}"
+
+
+SMALL_CASES = [
+    # mode, B, T, H, Hkv, D, window
+    ("exact", 2, 4, 2, 1, 16, (4, 0)),
+    ("exact", 1, 1, 1, 1, 16, (-1, 0)),
+    ("exact", 2, 130, 4, 2, 32, (-1, 0)),
+    ("exact", 1, 257, 2, 2, 64, (40, 0)),
+    ("exact", 2, 200, 4, 1, 128, (-1, 0)),
+    ("exact", 1, 96, 2, 2, 128, (16, 7)),
+    ("exact", 1, 70, 2, 1, 64, (0, 0)),
+    ("exact", 1, 50, 2, 2, 32, (-1, 5)),
+    ("fast", 2, 4, 2, 1, 16, (4, 0)),
+    ("fast", 1, 1, 2, 1, 128, (-1, 0)),
+    ("fast", 2, 130, 4, 2, 32, (-1, 0)),
+    ("fast", 1, 257, 6, 2, 64, (40, 0)),
+    ("fast", 2, 300, 4, 1, 128, (-1, 0)),
+    ("fast", 1, 192, 2, 2, 128, (64, 0)),
+    ("fast", 1, 96, 2, 2, 128, (16, 7)),
+    ("fast", 1, 70, 2, 1, 64, (0, 0)),
+    ("fast", 1, 50, 2, 2, 32, (-1, 5)),
+    ("fast", 1, 129, 3, 3, 128, (1000, 1000)),
+]
+
+
+@pytest.mark.parametrize("case", SMALL_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_small_cases(gpu, case):
+    mode, B, T, H, Hkv, D, window = case
+    _check_case(gpu, mode, B, T, H, Hkv, D, window, seed=zlib.crc32(repr(case).encode()) % 1000)
+
+
+@pytest.mark.parametrize("mode", ["exact", "fast"])
+@pytest.mark.parametrize("T,D,window", [(300, 64, (-1, 0)), (517, 128, (100, 0)), (260, 128, (-1, 0))])
+def test_document_mask(gpu, mode, T, D, window):
+    pos = W.document_positions(T, 2, seed=T + D, mean=40, sigma=1.0, cap=200)
+    _check_case(gpu, mode, 2, T, 4, 2, D, window, positions=pos, seed=T)
+
+
+def test_fast_mode_storage_dtypes(gpu):
+    # O, dO and gradients stored in fp32 while Q/K/V are bf16.
+    _check_case(gpu, "fast", 1, 150, 4, 2, 128, (-1, 0), out_dtype=torch.float32, grad_dtype=torch.float32,
+                dout_dtype=torch.float32)
+    _check_case(gpu, "fast", 1, 150, 4, 2, 64, (-1, 0), out_dtype=torch.float32, grad_dtype=torch.bfloat16,
+                dout_dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("mode", ["exact", "fast"])
+def test_accumulate_and_overwrite(gpu, mode):
+    fast = mode == "fast"
+    A = MFMAFast() if fast else MFMAExact()
+    B, T, H, Hkv, D = 1, 150, 4, 2, 64
+    Q, K, V, dO = _inputs(7, B, T, H, Hkv, D, fast)
+    Qd, Kd, Vd, dOd = (_dev(x, fast, gpu) for x in (Q, K, V, dO))
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, (-1, 0))
+    base = [torch.randn(x.shape, device=gpu).to(x.dtype) for x in (Qd, Kd, Vd)]
+    fresh = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), accumulate=False, init=base)
+    added = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), accumulate=True, init=base)
+    torch.cuda.synchronize()
+    tol = 1e-6 if not fast else 1e-2
+    for f, a, b0 in zip(fresh, added, base):
+        e = rel_err(to_np(a), to_np(f) + to_np(b0))
+        assert e <= tol, e
+
+
+@pytest.mark.parametrize("mode", ["exact", "fast"])
+def test_deterministic(gpu, mode):
+    fast = mode == "fast"
+    A = MFMAFast() if fast else MFMAExact()
+    Q, K, V, dO = _inputs(11, 2, 333, 4, 2, 128, fast)
+    Qd, Kd, Vd, dOd = (_dev(x, fast, gpu) for x in (Q, K, V, dO))
+    r1 = gpu_forward(A, Qd, Kd, Vd, (-1, 0))
+    r2 = gpu_forward(A, Qd, Kd, Vd, (-1, 0))
+    g1 = gpu_backward(A, dOd, Qd, Kd, Vd, *r1, (-1, 0))
+    g2 = gpu_backward(A, dOd, Qd, Kd, Vd, *r1, (-1, 0))
+    torch.cuda.synchronize()
+    for x, y in zip(r1 + g1, r2 + g2):
+        assert torch.equal(x, y), "results must be bitwise reproducible"
+
+
+def test_cross_mix_statistics_contract(gpu):
+    """Oracle forward statistics fed to the GPU backward, and GPU statistics to
+    the oracle backward, agree: pins the meaning of l and m across the boundary."""
+    A = MFMAExact()
+    B, T, H, Hkv, D = 1, 200, 2, 1, 64
+    Q, K, V, dO = _inputs(3, B, T, H, Hkv, D, False)
+    O_r, l_r, m_r = R.forward(Q, K, V, (-1, 0))
+    Qd, Kd, Vd, dOd = (_dev(x, False, gpu) for x in (Q, K, V, dO))
+    Od, ld, md = (torch.from_numpy(x.astype(np.float32)).to(gpu) for x in (O_r, l_r, m_r))
+    g = gpu_backward(A, dOd, Qd, Kd, Vd, Od, ld, md, (-1, 0))
+    g_ref = R.backward(dO, Q, K, V, O_r, l_r, m_r, (-1, 0))
+    for x, r in zip(g, g_ref):
+        assert rel_err(to_np(x), r) <= 1e-4
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, (-1, 0))
+    g2 = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), (-1, 0))
+    for x, r in zip(g2, g_ref):
+        assert rel_err(x, r) <= 1e-4
+
+
+def test_gqa_equals_repeated_kv(gpu):
+    """GQA == MHA with K/V repeated per group; dK/dV(GQA) = group sums of dK/dV(MHA)."""
+    A = MFMAFast()
+    B, T, H, Hkv, D = 2, 256, 6, 2, 128
+    G = H // Hkv
+    Q, K, V, dO = _inputs(5, B, T, H, Hkv, D, True)
+    Kr, Vr = np.repeat(K, G, axis=2), np.repeat(V, G, axis=2)
+    args = [_dev(x, True, gpu) for x in (Q, K, V, dO, Kr, Vr)]
+    Qd, Kd, Vd, dOd, Krd, Vrd = args
+    O1, l1, m1 = gpu_forward(A, Qd, Kd, Vd, (-1, 0))
+    O2, l2, m2 = gpu_forward(A, Qd, Krd, Vrd, (-1, 0))
+    assert torch.equal(O1, O2) and torch.equal(l1, l2) and torch.equal(m1, m2)
+    g1 = gpu_backward(A, dOd, Qd, Kd, Vd, O1, l1, m1, (-1, 0), grad_dtype=torch.float32)
+    g2 = gpu_backward(A, dOd, Qd, Krd, Vrd, O2, l2, m2, (-1, 0), grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(g1[0], g2[0])
+    for a, b in zip(g1[1:], g2[1:]):
+        summed = to_np(b).reshape(B, T, Hkv, G, D).sum(axis=3)
+        assert rel_err(to_np(a), summed) <= 1e-5
+
+
+def test_document_mask_equals_segments(gpu):
+    """A packed row with the document mask equals attention run separately on each
+    document (the reference semantics per segment)."""
+    A = MFMAExact()
+    T, H, Hkv, D = 300, 2, 1, 64
+    lengths = [37, 120, 1, 64, 78]
+    pos = np.concatenate([np.arange(n, dtype=np.int32) for n in lengths])[None, :]
+    Q, K, V, dO = _inputs(9, 1, T, H, Hkv, D, False)
+    Qd, Kd, Vd, dOd = (_dev(x, False, gpu) for x in (Q, K, V, dO))
+    pos_d = torch.from_numpy(pos).to(gpu)
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, (-1, 0), pos_d)
+    g = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), pos_d)
+    t0 = 0
+    for n in lengths:
+        sl = slice(t0, t0 + n)
+        Os, ls, ms = gpu_forward(A, Qd[:, sl].contiguous(), Kd[:, sl].contiguous(), Vd[:, sl].contiguous(), (-1, 0))
+        gs = gpu_backward(A, dOd[:, sl].contiguous(), Qd[:, sl].contiguous(), Kd[:, sl].contiguous(),
+                          Vd[:, sl].contiguous(), Os, ls, ms, (-1, 0))
+        assert rel_err(to_np(O[:, sl]), to_np(Os)) <= 1e-6
+        assert np.max(np.abs(to_np(l[:, :, sl]) - to_np(ls))) <= 1e-5 * max(1.0, float(to_np(ls).max()))
+        for a, b in zip(g, gs):
+            assert rel_err(to_np(a[:, sl]), to_np(b)) <= 1e-5
+        t0 += n
+
+
+# ---------------------------------------------------------------------------
+# Full-size BASELINE workloads.
+
+
+def _segments(pos_row):
+    T = len(pos_row)
+    start = np.maximum(0, np.arange(T) - pos_row.astype(np.int64))
+    cuts = [0] + [t for t in range(1, T) if start[t] != start[t - 1]] + [T]
+    return [(cuts[i], cuts[i + 1]) for i in range(len(cuts) - 1)]
+
+
+def _oracle_slice(h, b, kv, G, window, O_gpu, l_gpu, m_gpu):
+    """Oracle fwd/bwd for batch row b and KV group kv (the group's G query heads)."""
+    heads = list(range(kv * G, (kv + 1) * G))
+    Q = h.Q[b:b + 1][:, :, heads]
+    K = h.K[b:b + 1][:, :, kv:kv + 1]
+    V = h.V[b:b + 1][:, :, kv:kv + 1]
+    dO = h.dO[b:b + 1][:, :, heads]
+    pos = None if h.positions is None else h.positions[b:b + 1]
+    Og = O_gpu[b:b + 1][:, :, heads]
+    lg = l_gpu[b:b + 1][:, heads]
+    mg = m_gpu[b:b + 1][:, heads]
+    if pos is not None and np.any(pos[0] != np.arange(pos.shape[1])):
+        # Packed documents: the reference attention on each document segment.
+        T = Q.shape[1]
+        O = np.zeros(Q.shape)
+        l = np.zeros((1, len(heads), T))
+        m = np.zeros((1, len(heads), T))
+        dQ, dK, dV = np.zeros(Q.shape), np.zeros(K.shape), np.zeros(V.shape)
+        for s, e in _segments(pos[0]):
+            o, ll, mm = R.forward(Q[:, s:e], K[:, s:e], V[:, s:e], window)
+            O[:, s:e], l[:, :, s:e], m[:, :, s:e] = o, ll, mm
+            gq, gk, gv = R.backward(dO[:, s:e], Q[:, s:e], K[:, s:e], V[:, s:e], Og[:, s:e], lg[:, :, s:e],
+                                    mg[:, :, s:e], window)
+            dQ[:, s:e], dK[:, s:e], dV[:, s:e] = gq, gk, gv
+        return (O, l, m), (dQ, dK, dV)
+    fwd = R.forward(Q, K, V, window, pos)
+    bwd = R.backward(dO, Q, K, V, Og, lg, mg, window, pos)
+    return fwd, bwd
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+def test_baseline_workload(gpu, name):
+    wl = W.WORKLOADS[name]
+    A = MFMAFast() if wl.mode == "fast" else MFMAExact()
+    tol = TOL[wl.mode]
+    G = wl.H // wl.Hkv
+    for layer in range(wl.layers):
+        say(f"workload {name} layer {layer} window {wl.windows[layer]}")
+        h = W.host_inputs(wl, layer)
+        dt = torch.bfloat16 if wl.mode == "fast" else torch.float32
+        Qd, Kd, Vd, dOd = (torch.from_numpy(x).to(gpu, dt).contiguous() for x in (h.Q, h.K, h.V, h.dO))
+        pos_d = None if h.positions is None else torch.from_numpy(h.positions).to(gpu)
+        O, l, m = gpu_forward(A, Qd, Kd, Vd, h.window, pos_d)
+        dQ, dK, dV = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, h.window, pos_d)
+        torch.cuda.synchronize()
+        On, ln, mn = to_np(O), to_np(l), to_np(m)
+        gn = [to_np(x) for x in (dQ, dK, dV)]
+        assert all(np.isfinite(x).all() for x in [On, ln, mn] + gn)
+        # Properties over the whole output: every query sees at least itself.
+        assert (ln >= 1.0 - 1e-6).all()
+        rows = sorted({0, wl.B - 1})
+        groups = sorted({0, wl.Hkv - 1})
+        for b in rows:
+            for kv in groups:
+                heads = list(range(kv * G, (kv + 1) * G))
+                (O_r, l_r, m_r), (dQ_r, dK_r, dV_r) = _oracle_slice(h, b, kv, G, h.window, On, ln, mn)
+                eO = rel_err(On[b:b + 1][:, :, heads], O_r)
+                eL = lse_err(ln[b:b + 1][:, heads], mn[b:b + 1][:, heads], l_r, m_r)
+                e = [rel_err(gn[0][b:b + 1][:, :, heads], dQ_r), rel_err(gn[1][b:b + 1][:, :, kv:kv + 1], dK_r),
+                     rel_err(gn[2][b:b + 1][:, :, kv:kv + 1], dV_r)]
+                say(f"  b={b} kv={kv}: O {eO:.2e} LSE {eL:.2e} dQ {e[0]:.2e} dK {e[1]:.2e} dV {e[2]:.2e}")
+                assert eO <= tol and eL <= TOL_LSE and max(e) <= tol

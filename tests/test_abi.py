@@ -1,0 +1,138 @@
+"""The C ABI (CPU only: no kernel is launched).
+
+The library loads without a GPU, exports every function include/ declares,
+and rejects invalid descriptors, null pointers and short workspaces on the
+host with the documented status codes and a message, before any launch.
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import femtochat_amd._lib as L
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "femtochat_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fc_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    lib = L.lib()
+    names = declared_functions()
+    assert len(names) >= 9, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in {HEADER.name} but not exported"
+
+
+def test_header_compiles_as_c_and_cpp():
+    for lang, cc in (("c", "gcc"), ("c++", "g++")):
+        r = subprocess.run([cc, "-x", lang, "-fsyntax-only", "-Wall", "-Werror", str(HEADER)], capture_output=True,
+                           text=True)
+        assert r.returncode == 0, r.stderr
+
+
+def test_abi_version_and_head_dims():
+    lib = L.lib()
+    assert lib.fc_abi_version() == 1
+    mask = lib.fc_attn_supported_head_dims()
+    dims = [16 * (i + 1) for i in range(8) if (mask >> i) & 1]
+    assert 16 in dims and 128 in dims
+
+
+def desc(**kw):
+    d = L.AttnDesc()
+    base = dict(D=128, H=4, Hkv=2, T=64, B=2, win_left=-1, win_right=0, mode=L.FC_MODE_FAST,
+                in_dtype=L.FC_BF16, out_dtype=L.FC_BF16, dout_dtype=L.FC_BF16, grad_dtype=L.FC_BF16, flags=0)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(d, k, v)
+    return d
+
+
+def ws_bytes(d, pass_=L.FC_PASS_BACKWARD, pos=0):
+    n = ctypes.c_size_t(0)
+    st = L.lib().fc_attn_workspace_bytes(ctypes.byref(d), pass_, pos, ctypes.byref(n))
+    return st, n.value
+
+
+BAD = [
+    (dict(H=5, Hkv=2), L.FC_ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(D=24), L.FC_ERR_INVALID_ARGUMENT, "head_dim"),
+    (dict(D=256), L.FC_ERR_INVALID_ARGUMENT, "head_dim"),
+    (dict(D=48), L.FC_ERR_UNSUPPORTED, "not compiled"),
+    (dict(T=0), L.FC_ERR_INVALID_ARGUMENT, "positive"),
+    (dict(B=-1), L.FC_ERR_INVALID_ARGUMENT, "positive"),
+    (dict(mode=7), L.FC_ERR_INVALID_ARGUMENT, "mode"),
+    (dict(in_dtype=L.FC_F32), L.FC_ERR_INVALID_ARGUMENT, "bfloat16"),
+    (dict(mode=L.FC_MODE_EXACT), L.FC_ERR_INVALID_ARGUMENT, "float32"),
+    (dict(out_dtype=9), L.FC_ERR_INVALID_ARGUMENT, "dtype"),
+    (dict(flags=0x10), L.FC_ERR_INVALID_ARGUMENT, "flag"),
+]
+
+
+@pytest.mark.parametrize("kw,status,msg", BAD, ids=[str(b[0]) for b in BAD])
+def test_invalid_descriptors(kw, status, msg):
+    st, _ = ws_bytes(desc(**kw))
+    assert st == status
+    assert msg in L.lib().fc_last_error().decode()
+    fake = ctypes.c_void_p(0x1000)
+    st = L.lib().fc_attn_fwd(ctypes.byref(desc(**kw)), fake, fake, fake, None, fake, fake, fake, None, 0, None)
+    assert st == status
+
+
+def test_null_descriptor_and_pointers():
+    lib = L.lib()
+    n = ctypes.c_size_t(0)
+    assert lib.fc_attn_workspace_bytes(None, 0, 0, ctypes.byref(n)) == L.FC_ERR_INVALID_ARGUMENT
+    fake = ctypes.c_void_p(0x1000)
+    d = desc()
+    assert lib.fc_attn_fwd(ctypes.byref(d), None, fake, fake, None, fake, fake, fake, None, 0, None) == \
+        L.FC_ERR_INVALID_ARGUMENT
+    assert "null" in lib.fc_last_error().decode()
+    st = lib.fc_attn_bwd(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, None, None, fake, fake, fake,
+                         0, None)
+    assert st == L.FC_ERR_INVALID_ARGUMENT
+
+
+def test_workspace_checks():
+    lib = L.lib()
+    d = desc()
+    st, need = ws_bytes(d)
+    assert st == L.FC_OK and need > 0
+    st, fwd = ws_bytes(d, L.FC_PASS_FORWARD)
+    assert st == L.FC_OK and fwd == 0
+    # delta + lse2 (fp32 per query) at least; positions add the chunk bounds.
+    assert need >= 2 * 4 * d.B * d.H * d.T
+    _, need_pos = ws_bytes(d, pos=1)
+    assert need_pos > need
+    # fp32 dO in fast mode adds a bf16 copy of dO.
+    _, need_f32 = ws_bytes(desc(dout_dtype=L.FC_F32))
+    assert need_f32 >= need + 2 * d.B * d.T * d.H * d.D
+    fake = ctypes.c_void_p(0x1000)
+    st = lib.fc_attn_bwd(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake, fake,
+                         need - 1, None)
+    assert st == L.FC_ERR_WORKSPACE
+    assert str(need) in lib.fc_last_error().decode()
+    st = lib.fc_attn_bwd(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, None, fake, fake, fake,
+                         ctypes.c_void_p(0x1001), need, None)
+    assert st == L.FC_ERR_WORKSPACE and "aligned" in lib.fc_last_error().decode()
+
+
+def test_last_error_is_cleared_on_success():
+    lib = L.lib()
+    ws_bytes(desc(H=5, Hkv=2))
+    assert lib.fc_last_error().decode() != ""
+    st, _ = ws_bytes(desc())
+    assert st == L.FC_OK and lib.fc_last_error().decode() == ""
+
+
+def test_profile_collect_empty():
+    L.profile_enable(False)
+    assert L.profile_collect() == {}

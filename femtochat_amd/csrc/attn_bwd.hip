@@ -583,12 +583,12 @@ static hipError_t launch_dq_t(const Problem& p, const BwdArgs& a, hipStream_t s)
   }
 
 hipError_t launch_bwd_dkdv(const Problem& p, const BwdArgs& a, hipStream_t s) {
-  if (p.bf16) { FC_DISPATCH_D(launch_dkdv_t, bf16) }
+  if (p.bf16) return launch_bwd_dkdv_fast(p, a, s);
   FC_DISPATCH_D(launch_dkdv_t, float)
 }
 
 hipError_t launch_bwd_dq(const Problem& p, const BwdArgs& a, hipStream_t s) {
-  if (p.bf16) { FC_DISPATCH_D(launch_dq_t, bf16) }
+  if (p.bf16) return launch_bwd_dq_fast(p, a, s);
   FC_DISPATCH_D(launch_dq_t, float)
 }
 

@@ -1,0 +1,489 @@
+// Flash-attention backward, fast mode (bf16 inputs, fp32 accumulation), gfx950.
+//
+// Semantics as the exact-mode kernels (attn_bwd.hip, which also holds the
+// preprocess) and the reference backward (src/kernels.jl:287-379; P and dS
+// rounded to bf16 before their second product and dS = 0 for a query with a
+// single visible key, ext/FemtoChatCUDAExt.jl:1915-1946).
+//
+//  * attn_bwd_dkdv_fast: a workgroup owns 128 keys of one (batch, KV head);
+//    each wave keeps its 32 keys' K and V in registers (B operands of
+//    S = Q K^T and dP = dO V^T), loops over the GQA group's heads and the query
+//    tiles (64 queries) that can see the keys, and accumulates dK and dV in
+//    registers.  Q and dO tiles are staged once into swizzled LDS and read both
+//    as natural fragments (for S, dP) and through ds_read_b64_tr_b16 (for
+//    dV += P^T dO and dK += dS^T Q).
+//  * attn_bwd_dq_fast: a workgroup owns 128 queries of one (batch, head);
+//    S^T and dP^T are recomputed with the query as the lane index so dS^T is
+//    directly the B operand of dQ^T += K^T dS^T; K and V tiles are staged once
+//    and K is also read transposed.
+#include "attn_fast.hpp"
+#include "attn_launch.hpp"
+
+namespace fc {
+
+template <int D>
+struct DkdvFastCfg {
+  static constexpr int kBK = 128;  // keys per workgroup
+  static constexpr int kBQ = 64;   // queries per step
+  static constexpr int kKC = D / 16;
+  static constexpr int kDB = D < 32 ? 1 : D / 32;
+  static constexpr int kTileBytes = kBQ * 2 * D;
+  static constexpr int kStageBytes = 2 * kTileBytes;  // Q, dO
+};
+
+// One step of the dK/dV kernel: the wave's 32 keys against one staged tile
+// of BQ queries, processed 32 queries at a time.
+template <int D>
+struct DkdvStep {
+  using C = DkdvFastCfg<D>;
+  using M = Mma<bf16>;
+  static constexpr int BQ = C::kBQ, KC = C::kKC, DB = C::kDB, NQB = BQ / 32;
+
+  __device__ static inline void run(const char* Qs, const char* Os, const float* lse, const float* delta,
+                                    const int* lbs, const bf16x8* kf, const bf16x8* vf, f32x16* dk, f32x16* dv,
+                                    const FragOffsets<D>& fo, int q0, int key, int kw0, int kw1, int g, int lane,
+                                    int T, int right, float c2) {
+    const int lbv = lane < BQ ? lbs[lane] : lbs[0];
+    const int lbmin = wave_min64(lbv), lbmax = wave_max64(lbv);
+    const int ubmin = q0 + BQ - 1 >= T ? -1 : key_ub(q0, T, right);  // ub is monotone in q
+    const int ubmax = key_ub(min(q0 + BQ - 1, T - 1), T, right);
+    if (lbmin > kw1 || ubmax < kw0) return;
+    const bool need_mask = !(lbmax <= kw0 && kw1 <= ubmin);
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const bf16x8 qfrag = as_bf16x8(lds_load16(Qs + 32 * qb * 2 * D, fo.nat(c)));
+        const bf16x8 ofrag = as_bf16x8(lds_load16(Os + 32 * qb * 2 * D, fo.nat(c)));
+        s = M::mma(qfrag, kf[c], s);
+        dp = M::mma(ofrag, vf[c], dp);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i0 = 32 * qb + 8 * j + 4 * g;
+        const f32x4 L = *reinterpret_cast<const f32x4*>(&lse[i0]);
+        const f32x4 Dl = *reinterpret_cast<const f32x4*>(&delta[i0]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = 4 * j + t;
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -L[t]));
+          float ds = p * (dp[r] - Dl[t]);
+          if (need_mask) {
+            const int lbq = lbs[i0 + t];
+            const int ubq = key_ub(q0 + i0 + t, T, right);
+            const bool vis = key >= lbq && key <= ubq;
+            p = vis ? p : 0.0f;
+            ds = (vis && ubq > lbq) ? ds : 0.0f;
+          }
+          s[r] = p;
+          dp[r] = ds;
+        }
+      }
+      const bf16x8 pf0 = M::from_acc<0>(s), pf1 = M::from_acc<1>(s);
+      const bf16x8 sf0 = M::from_acc<0>(dp), sf1 = M::from_acc<1>(dp);
+      // dV += P^T dO and dK += dS^T Q for the 2 chunks of 16 queries of this block.
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kc = 2 * qb + h;
+        const char* qchunk = Qs + 16 * kc * 2 * D;
+        const char* ochunk = Os + 16 * kc * 2 * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16x8 ofr = lds_tr_frag(ochunk, fo.tr(0, db), fo.tr(1, db));
+          dv[db] = M::mma(h ? pf1 : pf0, ofr, dv[db]);
+          const bf16x8 qfr = lds_tr_frag(qchunk, fo.tr(0, db), fo.tr(1, db));
+          dk[db] = M::mma(h ? sf1 : sf0, qfr, dk[db]);
+        }
+      }
+    }
+  }
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs a) {
+  using C = DkdvFastCfg<D>;
+  constexpr int BQ = C::kBQ, KC = C::kKC, DB = C::kDB;
+  // Two stage buffers as distinct objects, so the compiler can tell the LDS
+  // loads of one from the DMA writes into the other.
+  __shared__ __attribute__((aligned(1024))) char bufA[C::kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char bufB[C::kStageBytes];
+  __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
+  __shared__ __attribute__((aligned(16))) float s_delta[2][BQ];
+  __shared__ __attribute__((aligned(16))) int s_lb[2][BQ];
+  constexpr int kVisTiles = 256;  // query tiles whose visibility is tabulated in LDS
+  __shared__ unsigned char s_vis[kVisTiles];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int T = a.T;
+  const int n_kt = (T + C::kBK - 1) / C::kBK;
+  const int id = xcd_remap(blockIdx.x, n_kt * a.Hkv * a.B);
+  const int bkv = id / n_kt;
+  const int kt = id - bkv * n_kt;
+  const int b = bkv / a.Hkv, kvh = bkv - b * a.Hkv;
+  const int k0 = kt * C::kBK;
+  const int k1 = min(k0 + C::kBK, T) - 1;
+  const int kw0 = k0 + 32 * wave, kw1 = kw0 + 31;
+  const int key = kw0 + l32;
+
+  const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;
+  const int64_t qrec = (int64_t)(T - 1) * qpitch + 2 * D;
+  const int64_t krec = (int64_t)(T - 1) * kpitch + 2 * D;
+  const char* Kb = static_cast<const char*>(a.K) + (((int64_t)b * T * a.Hkv + kvh) * D) * 2;
+  const char* Vb = static_cast<const char*>(a.V) + (((int64_t)b * T * a.Hkv + kvh) * D) * 2;
+  const int32_t* pos = a.pos ? a.pos + (int64_t)b * T : nullptr;
+  const int nchunks = (T + 31) / 32;
+  const int32_t* clb = a.chunk_lb ? a.chunk_lb + (int64_t)b * nchunks * 2 : nullptr;
+
+  // K and V of the wave's 32 keys as B operands (lane = key).
+  bf16x8 kf[KC], vf[KC];
+  {
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kb, (uint32_t)krec);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vb, (uint32_t)krec);
+    const int koff = key * kpitch + 16 * g;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      kf[c] = as_bf16x8(buf_load16(rk, koff + 32 * c, 0));
+      vf[c] = as_bf16x8(buf_load16(rv, koff + 32 * c, 0));
+    }
+  }
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) {
+    dk[i] = zero16();
+    dv[i] = zero16();
+  }
+
+  // Query tiles that can see [k0, k1]: q in [k0 - right, k1 + left].
+  const int qlo = max(0, k0 - a.right);
+  const int qhi = min(T - 1, k1 + a.left);
+  const int qt_begin = qlo / BQ;
+  const int n_qt_tiles = qhi >= qlo ? qhi / BQ - qt_begin + 1 : 0;
+  const int total_steps = n_qt_tiles * a.group;
+  // With positions, a query tile is skipped when no query of it can see a key
+  // of [k0, k1] (its smallest key lower bound exceeds k1).  The answers are
+  // tabulated in LDS up front so the step loop reads no global memory.
+  auto tile_visible_global = [&](int qt) -> bool {
+    const int c0 = (qt * BQ) / 32;
+    int lo = clb[2 * c0];
+#pragma unroll
+    for (int c = 1; c < BQ / 32; ++c)
+      if (c0 + c < nchunks) lo = min(lo, clb[2 * (c0 + c)]);
+    return lo <= k1;
+  };
+  const bool vis_table = clb != nullptr && n_qt_tiles <= kVisTiles;
+  if (vis_table) {
+    for (int t = tid; t < n_qt_tiles; t += kThreads) s_vis[t] = tile_visible_global(qt_begin + t) ? 1 : 0;
+  }
+  __syncthreads();
+  auto tile_visible = [&](int qt) -> bool {
+    if (clb == nullptr) return true;
+    return vis_table ? s_vis[qt - qt_begin] != 0 : tile_visible_global(qt);
+  };
+  auto next_step = [&](int st) -> int {
+    while (st < total_steps && !tile_visible(qt_begin + st % n_qt_tiles)) ++st;
+    return st;
+  };
+
+  FragOffsets<D> fo;
+  fo.init(lane);
+  DmaPlan<D, BQ> plan;
+  plan.init(wave, lane, qpitch);
+  float st_lse = 0.0f, st_delta = 0.0f;
+  int st_q = 0, st_pos = 0;
+  const float c2 = a.scale_log2;
+
+  // Starts loading step st: Q and dO tiles by DMA into buf, the row
+  // statistics and positions into registers.  publish() consumes them after
+  // the step's compute, so no wait on these loads sits in front of it.
+  auto issue = [&](int st, char* buf) {
+    const int h = kvh * a.group + st / n_qt_tiles;
+    const int q0 = (qt_begin + st % n_qt_tiles) * BQ;
+    const int64_t hoff = (((int64_t)b * T * a.H + h) * D) * 2;
+    const uint32_t at = lds_addr(buf);
+    plan.issue(tile_words(static_cast<const char*>(a.Q) + hoff, qrec, (int64_t)q0 * qpitch), at, wave);
+    plan.issue(tile_words(static_cast<const char*>(a.dO) + hoff, qrec, (int64_t)q0 * qpitch), at + C::kTileBytes,
+               wave);
+    if (tid < BQ) {
+      const int qq = q0 + tid;
+      const int64_t si = ((int64_t)b * a.H + h) * T + qq;
+      st_q = qq;
+      st_lse = qq < T ? a.lse2[si] : INFINITY;
+      st_delta = qq < T ? a.delta[si] : 0.0f;
+      st_pos = (pos != nullptr && qq < T) ? pos[qq] : 0;
+    }
+  };
+  auto publish = [&](int slot) {
+    if (tid < BQ) {
+      s_lse[slot][tid] = st_lse;
+      s_delta[slot][tid] = st_delta;
+      int lb = T;
+      if (st_q < T) lb = max(0, max(st_q - a.left, pos != nullptr ? st_q - st_pos : 0));
+      s_lb[slot][tid] = lb;
+    }
+  };
+  auto compute = [&](int st, const char* buf, int slot) {
+    const int q0 = (qt_begin + st % n_qt_tiles) * BQ;
+    DkdvStep<D>::run(buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], kf, vf, dk, dv, fo, q0, key,
+                     kw0, kw1, g, lane, T, a.right, c2);
+  };
+
+  int st = next_step(0);
+  if (st < total_steps) {
+    issue(st, bufA);
+    publish(0);
+  }
+  dma_wait_barrier();
+  while (st < total_steps) {
+    const int st1 = next_step(st + 1);
+    if (st1 < total_steps) issue(st1, bufB);
+    compute(st, bufA, 0);
+    if (st1 < total_steps) publish(1);
+    dma_wait_barrier();
+    if (st1 >= total_steps) break;
+    const int st2 = next_step(st1 + 1);
+    if (st2 < total_steps) issue(st2, bufA);
+    compute(st1, bufB, 1);
+    if (st2 < total_steps) publish(0);
+    dma_wait_barrier();
+    st = st2;
+  }
+
+  // Accumulator row = key, column = head-dim index.
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int d = 32 * db + l32;
+    if (d < D) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = kw0 + acc_row(r, g);
+        if (kk < T) {
+          const int64_t off = ((int64_t)b * T + kk) * a.Hkv * D + (int64_t)kvh * D + d;
+          float vk = dk[db][r] * a.scale, vv = dv[db][r];
+          if (a.grad_bf16) {
+            bf16* pk = static_cast<bf16*>(a.dK) + off;
+            bf16* pv = static_cast<bf16*>(a.dV) + off;
+            if (a.accumulate) {
+              vk += to_f32(*pk);
+              vv += to_f32(*pv);
+            }
+            *pk = static_cast<bf16>(vk);
+            *pv = static_cast<bf16>(vv);
+          } else {
+            float* pk = static_cast<float*>(a.dK) + off;
+            float* pv = static_cast<float*>(a.dV) + off;
+            if (a.accumulate) {
+              vk += *pk;
+              vv += *pv;
+            }
+            *pk = vk;
+            *pv = vv;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int D>
+struct DqFastCfg {
+  static constexpr int kBM = 128;  // queries per workgroup
+  static constexpr int kBN = 64;   // keys per tile
+  static constexpr int kKC = D / 16;
+  static constexpr int kDB = D < 32 ? 1 : D / 32;
+  static constexpr int kTileBytes = kBN * 2 * D;
+  static constexpr int kStageBytes = 2 * kTileBytes;  // K, V
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a) {
+  using C = DqFastCfg<D>;
+  using M = Mma<bf16>;
+  constexpr int BN = C::kBN, KC = C::kKC, DB = C::kDB, NKB = BN / 32;
+  __shared__ __attribute__((aligned(1024))) char bufA[C::kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char bufB[C::kStageBytes];
+  __shared__ int s_bounds[2][kWaves];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int T = a.T;
+  const int n_qt = (T + C::kBM - 1) / C::kBM;
+  const int id = xcd_remap(blockIdx.x, n_qt * a.H * a.B);
+  const int bh = id / n_qt;
+  const int qt = n_qt - 1 - (id - bh * n_qt);
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int kvh = h / a.group;
+
+  const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;
+  const int64_t qrec = (int64_t)(T - 1) * qpitch + 2 * D;
+  const int64_t krec = (int64_t)(T - 1) * kpitch + 2 * D;
+  const int64_t hoff = (((int64_t)b * T * a.H + h) * D) * 2;
+  const char* Kb = static_cast<const char*>(a.K) + (((int64_t)b * T * a.Hkv + kvh) * D) * 2;
+  const char* Vb = static_cast<const char*>(a.V) + (((int64_t)b * T * a.Hkv + kvh) * D) * 2;
+  const int32_t* pos = a.pos ? a.pos + (int64_t)b * T : nullptr;
+
+  const int q = qt * C::kBM + wave * 32 + l32;
+  const int lb = key_lb(q, T, a.left, pos), ub = key_ub(q, T, a.right);
+  const bool multiple = ub > lb;
+  const int wlb_min = wave_min32(lb), wlb_max = wave_max32(lb);
+  const int wub_min = wave_min32(ub), wub_max = wave_max32(ub);
+  if (lane == 0) {
+    s_bounds[0][wave] = wlb_min;
+    s_bounds[1][wave] = wub_max;
+  }
+  const int64_t si = ((int64_t)b * a.H + h) * T + q;
+  const float neg_lse = q < T ? -a.lse2[si] : -INFINITY;
+  const float dlt = q < T ? a.delta[si] : 0.0f;
+
+  bf16x8 qf[KC], of[KC];
+  {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(static_cast<const char*>(a.Q) + hoff, (uint32_t)qrec);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<const char*>(a.dO) + hoff, (uint32_t)qrec);
+    const int qoff = q * qpitch + 16 * g;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      qf[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c, 0));
+      of[c] = as_bf16x8(buf_load16(ro, qoff + 32 * c, 0));
+    }
+  }
+  FragOffsets<D> fo;
+  fo.init(lane);
+  DmaPlan<D, BN> plan;
+  plan.init(wave, lane, kpitch);
+  f32x16 dq[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) dq[i] = zero16();
+  const float c2 = a.scale_log2;
+
+  __syncthreads();
+  int kmin = s_bounds[0][0], kmax = s_bounds[1][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    kmin = min(kmin, s_bounds[0][w]);
+    kmax = max(kmax, s_bounds[1][w]);
+  }
+  const int kt0 = (kmin / BN) * BN;
+  const int ntiles = kmax >= kmin ? (kmax - kt0) / BN + 1 : 0;
+
+  auto issue = [&](int it, char* buf) {
+    const int64_t row0 = (int64_t)(kt0 + it * BN) * kpitch;
+    const uint32_t at = lds_addr(buf);
+    plan.issue(tile_words(Kb, krec, row0), at, wave);
+    plan.issue(tile_words(Vb, krec, row0), at + C::kTileBytes, wave);
+  };
+  auto compute = [&](int it, const char* Ks) {
+    const int kt = kt0 + it * BN;
+    if (wlb_min > kt + BN - 1 || wub_max < kt) return;
+    const char* Vs = Ks + C::kTileBytes;
+    const bool need_mask = !(wlb_max <= kt && kt + BN - 1 <= wub_min);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const bf16x8 kfrag = as_bf16x8(lds_load16(Ks + 32 * kb * 2 * D, fo.nat(c)));
+        const bf16x8 vfrag = as_bf16x8(lds_load16(Vs + 32 * kb * 2 * D, fo.nat(c)));
+        s = M::mma(kfrag, qf[c], s);
+        dp = M::mma(vfrag, of[c], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, neg_lse));
+        float ds = p * (dp[r] - dlt);
+        if (need_mask) {
+          const int kk = kt + 32 * kb + acc_row(r, g);
+          ds = (kk >= lb && kk <= ub && multiple) ? ds : 0.0f;
+        }
+        dp[r] = ds;
+      }
+      const bf16x8 sf0 = M::from_acc<0>(dp), sf1 = M::from_acc<1>(dp);
+      // dQ^T += K^T dS^T for the 2 chunks of 16 keys of this block.
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const char* kchunk = Ks + 16 * (2 * kb + hh) * 2 * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16x8 kfr = lds_tr_frag(kchunk, fo.tr(0, db), fo.tr(1, db));
+          dq[db] = M::mma(kfr, hh ? sf1 : sf0, dq[db]);
+        }
+      }
+    }
+  };
+
+  if (ntiles > 0) issue(0, bufA);
+  dma_wait_barrier();
+  for (int it = 0; it < ntiles; it += 2) {
+    if (it + 1 < ntiles) issue(it + 1, bufB);
+    compute(it, bufA);
+    dma_wait_barrier();
+    if (it + 1 >= ntiles) break;
+    if (it + 2 < ntiles) issue(it + 2, bufA);
+    compute(it + 1, bufB);
+    dma_wait_barrier();
+  }
+
+  if (q < T) {
+    const int64_t orow = ((int64_t)b * T + q) * a.H + h;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 32 * db + 8 * j + 4 * g;
+        if (d0 < D) {
+          f32x4 v;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = dq[db][4 * j + t] * a.scale;
+          if (a.grad_bf16) store4(static_cast<bf16*>(a.dQ) + orow * D + d0, v, a.accumulate);
+          else store4(static_cast<float*>(a.dQ) + orow * D + d0, v, a.accumulate);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int D>
+static hipError_t launch_dkdv_fast_t(const Problem& p, const BwdArgs& a, hipStream_t s) {
+  const int n_kt = (p.T + DkdvFastCfg<D>::kBK - 1) / DkdvFastCfg<D>::kBK;
+  const dim3 grid(n_kt * p.Hkv * p.B), block(kThreads);
+  const ProfileMark mk = profile_begin(s);
+  hipLaunchKernelGGL((attn_bwd_dkdv_fast_kernel<D>), grid, block, 0, s, a);
+  const hipError_t e = hipGetLastError();
+  profile_end(mk, "attn_bwd_dkdv_bf16", s);
+  return e;
+}
+
+template <int D>
+static hipError_t launch_dq_fast_t(const Problem& p, const BwdArgs& a, hipStream_t s) {
+  const int n_qt = (p.T + DqFastCfg<D>::kBM - 1) / DqFastCfg<D>::kBM;
+  const dim3 grid(n_qt * p.H * p.B), block(kThreads);
+  const ProfileMark mk = profile_begin(s);
+  hipLaunchKernelGGL((attn_bwd_dq_fast_kernel<D>), grid, block, 0, s, a);
+  const hipError_t e = hipGetLastError();
+  profile_end(mk, "attn_bwd_dq_bf16", s);
+  return e;
+}
+
+hipError_t launch_bwd_dkdv_fast(const Problem& p, const BwdArgs& a, hipStream_t s) {
+  switch (p.D) {
+    case 16: return launch_dkdv_fast_t<16>(p, a, s);
+    case 32: return launch_dkdv_fast_t<32>(p, a, s);
+    case 64: return launch_dkdv_fast_t<64>(p, a, s);
+    case 128: return launch_dkdv_fast_t<128>(p, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_bwd_dq_fast(const Problem& p, const BwdArgs& a, hipStream_t s) {
+  switch (p.D) {
+    case 16: return launch_dq_fast_t<16>(p, a, s);
+    case 32: return launch_dq_fast_t<32>(p, a, s);
+    case 64: return launch_dq_fast_t<64>(p, a, s);
+    case 128: return launch_dq_fast_t<128>(p, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fc

@@ -235,7 +235,7 @@ static hipError_t launch_fwd_e(const Problem& p, const FwdArgs& a, hipStream_t s
 }
 
 hipError_t launch_fwd(const Problem& p, const FwdArgs& a, hipStream_t s) {
-  return p.bf16 ? launch_fwd_e<bf16>(p, a, s) : launch_fwd_e<float>(p, a, s);
+  return p.bf16 ? launch_fwd_fast(p, a, s) : launch_fwd_e<float>(p, a, s);
 }
 
 bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }

@@ -84,6 +84,10 @@ hipError_t launch_bwd_pre(const Problem& p, const PreArgs& a, hipStream_t s);
 hipError_t launch_bounds(const Problem& p, const BoundsArgs& a, hipStream_t s);
 hipError_t launch_bwd_dkdv(const Problem& p, const BwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_dq(const Problem& p, const BwdArgs& a, hipStream_t s);
+// Fast-mode (bf16) kernels, attn_fwd_fast.hip / attn_bwd_fast.hip.
+hipError_t launch_fwd_fast(const Problem& p, const FwdArgs& a, hipStream_t s);
+hipError_t launch_bwd_dkdv_fast(const Problem& p, const BwdArgs& a, hipStream_t s);
+hipError_t launch_bwd_dq_fast(const Problem& p, const BwdArgs& a, hipStream_t s);
 
 // Profiling hooks (attn_api.hip): bracket one launch with events when enabled.
 struct ProfileMark {

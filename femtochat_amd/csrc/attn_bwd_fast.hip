@@ -19,6 +19,8 @@
 #include "attn_fast.hpp"
 #include "attn_launch.hpp"
 
+#include <type_traits>
+
 namespace fc {
 
 template <int D>
@@ -48,7 +50,17 @@ struct DkdvStep {
     const int ubmin = q0 + BQ - 1 >= T ? -1 : key_ub(q0, T, right);  // ub is monotone in q
     const int ubmax = key_ub(min(q0 + BQ - 1, T - 1), T, right);
     if (lbmin > kw1 || ubmax < kw0) return;
-    const bool need_mask = !(lbmax <= kw0 && kw1 <= ubmin);
+    // Two straight-line bodies: tiles inside every window skip the mask.
+    if (lbmax <= kw0 && kw1 <= ubmin)
+      body<false>(Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+    else
+      body<true>(Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+  }
+
+  template <bool need_mask>
+  __device__ static inline void body(const char* Qs, const char* Os, const float* lse, const float* delta,
+                                     const int* lbs, const bf16x8* kf, const bf16x8* vf, f32x16* dk, f32x16* dv,
+                                     const FragOffsets<D>& fo, int q0, int key, int g, int T, int right, float c2) {
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
       f32x16 s = zero16(), dp = zero16();
@@ -160,7 +172,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   const int qhi = min(T - 1, k1 + a.left);
   const int qt_begin = qlo / BQ;
   const int n_qt_tiles = qhi >= qlo ? qhi / BQ - qt_begin + 1 : 0;
-  const int total_steps = n_qt_tiles * a.group;
   // With positions, a query tile is skipped when no query of it can see a key
   // of [k0, k1] (its smallest key lower bound exceeds k1).  The answers are
   // tabulated in LDS up front so the step loop reads no global memory.
@@ -181,9 +192,19 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
     if (clb == nullptr) return true;
     return vis_table ? s_vis[qt - qt_begin] != 0 : tile_visible_global(qt);
   };
-  auto next_step = [&](int st) -> int {
-    while (st < total_steps && !tile_visible(qt_begin + st % n_qt_tiles)) ++st;
-    return st;
+  // A step is (head of the group, query tile): heads outer, tiles inner,
+  // invisible tiles skipped.  step.h == group marks the end.
+  struct Step {
+    int h, t;
+  };
+  auto first_tile = [&](int t) -> int {
+    while (t < n_qt_tiles && !tile_visible(qt_begin + t)) ++t;
+    return t;
+  };
+  const int t_first = first_tile(0);
+  auto advance = [&](Step s) -> Step {
+    const int t = first_tile(s.t + 1);
+    return t < n_qt_tiles ? Step{s.h, t} : Step{s.h + 1, t_first};
   };
 
   FragOffsets<D> fo;
@@ -197,9 +218,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   // Starts loading step st: Q and dO tiles by DMA into buf, the row
   // statistics and positions into registers.  publish() consumes them after
   // the step's compute, so no wait on these loads sits in front of it.
-  auto issue = [&](int st, char* buf) {
-    const int h = kvh * a.group + st / n_qt_tiles;
-    const int q0 = (qt_begin + st % n_qt_tiles) * BQ;
+  auto issue = [&](Step st, char* buf) {
+    const int h = kvh * a.group + st.h;
+    const int q0 = (qt_begin + st.t) * BQ;
     const int64_t hoff = (((int64_t)b * T * a.H + h) * D) * 2;
     const uint32_t at = lds_addr(buf);
     plan.issue(tile_words(static_cast<const char*>(a.Q) + hoff, qrec, (int64_t)q0 * qpitch), at, wave);
@@ -223,29 +244,30 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       s_lb[slot][tid] = lb;
     }
   };
-  auto compute = [&](int st, const char* buf, int slot) {
-    const int q0 = (qt_begin + st % n_qt_tiles) * BQ;
+  auto compute = [&](Step st, const char* buf, int slot) {
+    const int q0 = (qt_begin + st.t) * BQ;
     DkdvStep<D>::run(buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], kf, vf, dk, dv, fo, q0, key,
                      kw0, kw1, g, lane, T, a.right, c2);
   };
 
-  int st = next_step(0);
-  if (st < total_steps) {
+  const int G = t_first < n_qt_tiles ? a.group : 0;  // no visible tile: no step
+  Step st{0, t_first};
+  if (st.h < G) {
     issue(st, bufA);
     publish(0);
   }
   dma_wait_barrier();
-  while (st < total_steps) {
-    const int st1 = next_step(st + 1);
-    if (st1 < total_steps) issue(st1, bufB);
+  while (st.h < G) {
+    const Step st1 = advance(st);
+    if (st1.h < G) issue(st1, bufB);
     compute(st, bufA, 0);
-    if (st1 < total_steps) publish(1);
+    if (st1.h < G) publish(1);
     dma_wait_barrier();
-    if (st1 >= total_steps) break;
-    const int st2 = next_step(st1 + 1);
-    if (st2 < total_steps) issue(st2, bufA);
+    if (st1.h >= G) break;
+    const Step st2 = advance(st1);
+    if (st2.h < G) issue(st2, bufA);
     compute(st1, bufB, 1);
-    if (st2 < total_steps) publish(0);
+    if (st2.h < G) publish(0);
     dma_wait_barrier();
     st = st2;
   }
@@ -373,11 +395,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
     plan.issue(tile_words(Kb, krec, row0), at, wave);
     plan.issue(tile_words(Vb, krec, row0), at + C::kTileBytes, wave);
   };
-  auto compute = [&](int it, const char* Ks) {
-    const int kt = kt0 + it * BN;
-    if (wlb_min > kt + BN - 1 || wub_max < kt) return;
+  auto body = [&](auto mask_tag, int kt, const char* Ks) {
+    constexpr bool need_mask = decltype(mask_tag)::value;
     const char* Vs = Ks + C::kTileBytes;
-    const bool need_mask = !(wlb_max <= kt && kt + BN - 1 <= wub_min);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       f32x16 s = zero16(), dp = zero16();
@@ -410,6 +430,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
         }
       }
     }
+  };
+  auto compute = [&](int it, const char* Ks) {
+    const int kt = kt0 + it * BN;
+    if (wlb_min > kt + BN - 1 || wub_max < kt) return;
+    if (wlb_max <= kt && kt + BN - 1 <= wub_min) body(std::false_type{}, kt, Ks);
+    else body(std::true_type{}, kt, Ks);
   };
 
   if (ntiles > 0) issue(0, bufA);

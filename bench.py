@@ -51,6 +51,20 @@ def kernel_flops(name: str, D: int, pairs: int, B: int, T: int, H: int) -> tuple
     return "hbm", 0, "byte"
 
 
+def measured_traffic(workload: str) -> dict:
+    """HBM bytes per launch by kernel, from rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+    (scaled by a copy-kernel calibration) committed in profiles/."""
+    path = os.path.join(ROOT, "profiles", f"attn_{workload.lower()}_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except OSError:
+        return {}
+    if data.get("workload") != workload:
+        return {}
+    return {k: v["read_bytes"] + v["write_bytes"] for k, v in data.get("kernels", {}).items()}
+
+
 def cpu_baseline(wl, rows: int, threads: int) -> dict:
     """Time the reference's blocked FA-1 CPU algorithm (float32 restatement in
     oracle/fa1.c, 512-blocks, no skipping) on a bounded sample of the same
@@ -89,7 +103,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="C3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-rows", type=int, default=2)
+    ap.add_argument("--cpu-rows", type=int, default=16, help="batch rows in the CPU baseline sample")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this build has a single MI355X, and the attention "
@@ -157,8 +171,16 @@ def main() -> int:
     dominant = max(kernels.items(), key=lambda kv: kv[1][1])[0]
     dk = per_kernel[dominant]
     dpeak = peak if dk["bound"] == "mfma" else PEAK_HBM_GBS
+    traffic = measured_traffic(wl.name)
+    dom_key = next((k for k in traffic if dominant.startswith(k)), None)
     roofline = {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dpeak,
-                "unit": dk["unit"], "frac": round(dk["achieved"] / dpeak, 4), "traffic": None}
+                "unit": dk["unit"], "frac": round(dk["achieved"] / dpeak, 4),
+                "traffic": traffic[dom_key] if dom_key else None}
+    for name, rec in per_kernel.items():
+        key = next((k for k in traffic if name.startswith(k)), None)
+        if key:
+            rec["hbm_bytes"] = traffic[key]
+            rec["hbm_gbs"] = round(traffic[key] / (rec["avg_ms"] * 1e-3) / 1e9, 1)
 
     cpu = None
     if not args.no_cpu:

@@ -57,30 +57,71 @@ struct DkdvStep {
       body<true>(Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
   }
 
+  // Software-pipelined step body.  LDS fragments are loaded one stage ahead
+  // of the products that use them (sched_barrier keeps the order), and the
+  // transposed dO / Q fragments of a 32-query block are in flight while its
+  // softmax runs, so at one wave per SIMD the LDS latency hides behind work.
   template <bool need_mask>
   __device__ static inline void body(const char* Qs, const char* Os, const float* lse, const float* delta,
                                      const int* lbs, const bf16x8* kf, const bf16x8* vf, f32x16* dk, f32x16* dv,
                                      const FragOffsets<D>& fo, int q0, int key, int g, int T, int right, float c2) {
+    f32x16 s[NQB], dp[NQB];
+    bf16x8 qa[2][NQB], oa[2][NQB];
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-      f32x16 s = zero16(), dp = zero16();
+      s[qb] = zero16();
+      dp[qb] = zero16();
+      qa[0][qb] = as_bf16x8(lds_load16(Qs + 32 * qb * 2 * D, fo.nat(0)));
+      oa[0][qb] = as_bf16x8(lds_load16(Os + 32 * qb * 2 * D, fo.nat(0)));
+    }
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const bf16x8 qfrag = as_bf16x8(lds_load16(Qs + 32 * qb * 2 * D, fo.nat(c)));
-        const bf16x8 ofrag = as_bf16x8(lds_load16(Os + 32 * qb * 2 * D, fo.nat(c)));
-        s = M::mma(qfrag, kf[c], s);
-        dp = M::mma(ofrag, vf[c], dp);
+    for (int c = 0; c < KC; ++c) {
+      const int cur = c & 1, nxt = cur ^ 1;
+      if (c + 1 < KC) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+          qa[nxt][qb] = as_bf16x8(lds_load16(Qs + 32 * qb * 2 * D, fo.nat(c + 1)));
+          oa[nxt][qb] = as_bf16x8(lds_load16(Os + 32 * qb * 2 * D, fo.nat(c + 1)));
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        s[qb] = M::mma(qa[cur][qb], kf[c], s[qb]);
+        dp[qb] = M::mma(oa[cur][qb], vf[c], dp[qb]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      // Transposed fragments for this block's dV / dK products, loaded now.
+      bf16x8 ofr[2][DB], qfr[2][DB];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const char* qchunk = Qs + 16 * (2 * qb + h) * 2 * D;
+        const char* ochunk = Os + 16 * (2 * qb + h) * 2 * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          ofr[h][db] = lds_tr_frag(ochunk, fo.tr(0, db), fo.tr(1, db));
+          qfr[h][db] = lds_tr_frag(qchunk, fo.tr(0, db), fo.tr(1, db));
+        }
+      }
+      f32x4 L[4], Dl[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i0 = 32 * qb + 8 * j + 4 * g;
-        const f32x4 L = *reinterpret_cast<const f32x4*>(&lse[i0]);
-        const f32x4 Dl = *reinterpret_cast<const f32x4*>(&delta[i0]);
+        L[j] = *reinterpret_cast<const f32x4*>(&lse[i0]);
+        Dl[j] = *reinterpret_cast<const f32x4*>(&delta[i0]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i0 = 32 * qb + 8 * j + 4 * g;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int r = 4 * j + t;
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -L[t]));
-          float ds = p * (dp[r] - Dl[t]);
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c2, -L[j][t]));
+          float ds = p * (dp[qb][r] - Dl[j][t]);
           if (need_mask) {
             const int lbq = lbs[i0 + t];
             const int ubq = key_ub(q0 + i0 + t, T, right);
@@ -88,24 +129,18 @@ struct DkdvStep {
             p = vis ? p : 0.0f;
             ds = (vis && ubq > lbq) ? ds : 0.0f;
           }
-          s[r] = p;
-          dp[r] = ds;
+          s[qb][r] = p;
+          dp[qb][r] = ds;
         }
       }
-      const bf16x8 pf0 = M::from_acc<0>(s), pf1 = M::from_acc<1>(s);
-      const bf16x8 sf0 = M::from_acc<0>(dp), sf1 = M::from_acc<1>(dp);
-      // dV += P^T dO and dK += dS^T Q for the 2 chunks of 16 queries of this block.
+      const bf16x8 pf0 = M::from_acc<0>(s[qb]), pf1 = M::from_acc<1>(s[qb]);
+      const bf16x8 sf0 = M::from_acc<0>(dp[qb]), sf1 = M::from_acc<1>(dp[qb]);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int kc = 2 * qb + h;
-        const char* qchunk = Qs + 16 * kc * 2 * D;
-        const char* ochunk = Os + 16 * kc * 2 * D;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 ofr = lds_tr_frag(ochunk, fo.tr(0, db), fo.tr(1, db));
-          dv[db] = M::mma(h ? pf1 : pf0, ofr, dv[db]);
-          const bf16x8 qfr = lds_tr_frag(qchunk, fo.tr(0, db), fo.tr(1, db));
-          dk[db] = M::mma(h ? sf1 : sf0, qfr, dk[db]);
+          dv[db] = M::mma(h ? pf1 : pf0, ofr[h][db], dv[db]);
+          dk[db] = M::mma(h ? sf1 : sf0, qfr[h][db], dk[db]);
         }
       }
     }

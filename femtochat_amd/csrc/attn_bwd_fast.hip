@@ -41,109 +41,211 @@ struct DkdvStep {
   using M = Mma<bf16>;
   static constexpr int BQ = C::kBQ, KC = C::kKC, DB = C::kDB, NQB = BQ / 32;
 
-  __device__ static inline void run(const char* Qs, const char* Os, const float* lse, const float* delta,
-                                    const int* lbs, const bf16x8* kf, const bf16x8* vf, f32x16* dk, f32x16* dv,
-                                    const FragOffsets<D>& fo, int q0, int key, int kw0, int kw1, int g, int lane,
-                                    int T, int right, float c2) {
-    const int lbv = lane < BQ ? lbs[lane] : lbs[0];
-    const int lbmin = wave_min64(lbv), lbmax = wave_max64(lbv);
+  // dma(k), k = 0..3, issues a quarter of the next tile's loads; the body
+  // calls it at its phase boundaries so the loads queue behind the products
+  // instead of all at once.
+  template <typename Dma>
+  __device__ static inline void run(const Dma& dma, const char* Qs, const char* Os, const float* lse,
+                                    const float* delta,
+                                    const int* lbs, const int* lbmm, const bf16x8* kf, const bf16x8* vf,
+                                    f32x16* dk, f32x16* dv, const FragOffsets<D>& fo, int q0, int key, int kw0,
+                                    int kw1, int g, int T, int right, float c2) {
+    // Smallest and largest key lower bound over the tile's queries, tabulated
+    // when the tile was published (no cross-lane reduction in the step).
+    const int lbmin = lbmm[0], lbmax = lbmm[1];
     const int ubmin = q0 + BQ - 1 >= T ? -1 : key_ub(q0, T, right);  // ub is monotone in q
     const int ubmax = key_ub(min(q0 + BQ - 1, T - 1), T, right);
-    if (lbmin > kw1 || ubmax < kw0) return;
+    if (lbmin > kw1 || ubmax < kw0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dma(k);
+      return;
+    }
     // Two straight-line bodies: tiles inside every window skip the mask.
     if (lbmax <= kw0 && kw1 <= ubmin)
-      body<false>(Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+      body<false>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
     else
-      body<true>(Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+      body<true>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
   }
 
-  // Software-pipelined step body.  LDS fragments are loaded one stage ahead
-  // of the products that use them (sched_barrier keeps the order), and the
-  // transposed dO / Q fragments of a 32-query block are in flight while its
-  // softmax runs, so at one wave per SIMD the LDS latency hides behind work.
+  // Step body as four phases over the tile's two 32-query blocks A and B:
+  //   1. S, dP of A
+  //   2. S, dP of B      + softmax of A
+  //   3. dV, dK from A   + softmax of B
+  //   4. dV, dK from B
+  // At one wave per SIMD, a VALU instruction only overlaps an MFMA when it
+  // sits between MFMAs in the wave's own instruction stream, so each phase
+  // interleaves one MFMA with a few VALU and LDS instructions
+  // (sched_group_barrier), and each block's softmax runs under the products
+  // of the other block.  LDS fragments are requested a phase or a few
+  // products before their use.
   template <bool need_mask>
-  __device__ static inline void body(const char* Qs, const char* Os, const float* lse, const float* delta,
+  __device__ static inline void softmax(f32x16& s, f32x16& dp, const f32x4* L, const f32x4* Dl, const int* lbs,
+                                        int qb, int q0, int key, int g, int T, int right, float c2, bf16x8* pf,
+                                        bf16x8* sf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i0 = 32 * qb + 8 * j + 4 * g;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int r = 4 * j + t;
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -L[j][t]));
+        float ds = p * (dp[r] - Dl[j][t]);
+        if (need_mask) {
+          const int lbq = lbs[i0 + t];
+          const int ubq = key_ub(q0 + i0 + t, T, right);
+          const bool vis = key >= lbq && key <= ubq;
+          p = vis ? p : 0.0f;
+          ds = (vis && ubq > lbq) ? ds : 0.0f;
+        }
+        s[r] = p;
+        dp[r] = ds;
+      }
+    }
+    pf[0] = M::from_acc<0>(s);
+    pf[1] = M::from_acc<1>(s);
+    sf[0] = M::from_acc<0>(dp);
+    sf[1] = M::from_acc<1>(dp);
+  }
+
+  static constexpr int kSchedVALU = 0x2, kSchedMFMA = 0x8, kSchedDSRead = 0x100;
+  static constexpr int NTR = 2 * DB;  // transposed fragments per operand and block
+  static constexpr int NPRE = NTR < 2 ? NTR : 2;  // of them requested one phase early
+
+  __device__ static inline void stats(const float* lse, const float* delta, int qb, int g, f32x4* L, f32x4* Dl) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i0 = 32 * qb + 8 * j + 4 * g;
+      L[j] = *reinterpret_cast<const f32x4*>(&lse[i0]);
+      Dl[j] = *reinterpret_cast<const f32x4*>(&delta[i0]);
+    }
+  }
+
+  template <bool need_mask, typename Dma>
+  __device__ static inline void body(const Dma& dma, const char* Qs, const char* Os, const float* lse,
+                                     const float* delta,
                                      const int* lbs, const bf16x8* kf, const bf16x8* vf, f32x16* dk, f32x16* dv,
                                      const FragOffsets<D>& fo, int q0, int key, int g, int T, int right, float c2) {
-    f32x16 s[NQB], dp[NQB];
-    bf16x8 qa[2][NQB], oa[2][NQB];
+    static_assert(NQB == 2, "the phase schedule assumes two 32-query blocks per tile");
+    constexpr int M1 = 2 * KC;   // MFMAs of S, dP per block
+    constexpr int M2 = 2 * NTR;  // MFMAs of dV, dK per block
+    const char* QB = Qs + 32 * 2 * D;
+    const char* OB = Os + 32 * 2 * D;
+    f32x16 sA = zero16(), pA = zero16(), sB = zero16(), pB = zero16();
+    f32x4 LA[4], DA[4], LB[4], DB_[4];
+    bf16x8 pfA[2], sfA[2], pfB[2], sfB[2];
+    bf16x8 ofA[NTR], qfA[NTR], ofB[NTR], qfB[NTR];  // index h * DB + db
+
+    // Phase 1.
+    dma(0);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      bf16x8 qa[KC], oa[KC];
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-      s[qb] = zero16();
-      dp[qb] = zero16();
-      qa[0][qb] = as_bf16x8(lds_load16(Qs + 32 * qb * 2 * D, fo.nat(0)));
-      oa[0][qb] = as_bf16x8(lds_load16(Os + 32 * qb * 2 * D, fo.nat(0)));
-    }
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const int cur = c & 1, nxt = cur ^ 1;
-      if (c + 1 < KC) {
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-          qa[nxt][qb] = as_bf16x8(lds_load16(Qs + 32 * qb * 2 * D, fo.nat(c + 1)));
-          oa[nxt][qb] = as_bf16x8(lds_load16(Os + 32 * qb * 2 * D, fo.nat(c + 1)));
-        }
+      for (int c = 0; c < KC; ++c) {
+        qa[c] = as_bf16x8(lds_load16(Qs, fo.nat(c)));
+        oa[c] = as_bf16x8(lds_load16(Os, fo.nat(c)));
       }
-      __builtin_amdgcn_sched_barrier(0);
+      stats(lse, delta, 0, g, LA, DA);
 #pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        s[qb] = M::mma(qa[cur][qb], kf[c], s[qb]);
-        dp[qb] = M::mma(oa[cur][qb], vf[c], dp[qb]);
+      for (int c = 0; c < KC; ++c) {
+        sA = M::mma(qa[c], kf[c], sA);
+        pA = M::mma(oa[c], vf[c], pA);
       }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 6, 0);
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-      // Transposed fragments for this block's dV / dK products, loaded now.
-      bf16x8 ofr[2][DB], qfr[2][DB];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const char* qchunk = Qs + 16 * (2 * qb + h) * 2 * D;
-        const char* ochunk = Os + 16 * (2 * qb + h) * 2 * D;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          ofr[h][db] = lds_tr_frag(ochunk, fo.tr(0, db), fo.tr(1, db));
-          qfr[h][db] = lds_tr_frag(qchunk, fo.tr(0, db), fo.tr(1, db));
-        }
-      }
-      f32x4 L[4], Dl[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i0 = 32 * qb + 8 * j + 4 * g;
-        L[j] = *reinterpret_cast<const f32x4*>(&lse[i0]);
-        Dl[j] = *reinterpret_cast<const f32x4*>(&delta[i0]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i0 = 32 * qb + 8 * j + 4 * g;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int r = 4 * j + t;
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c2, -L[j][t]));
-          float ds = p * (dp[qb][r] - Dl[j][t]);
-          if (need_mask) {
-            const int lbq = lbs[i0 + t];
-            const int ubq = key_ub(q0 + i0 + t, T, right);
-            const bool vis = key >= lbq && key <= ubq;
-            p = vis ? p : 0.0f;
-            ds = (vis && ubq > lbq) ? ds : 0.0f;
-          }
-          s[qb][r] = p;
-          dp[qb][r] = ds;
-        }
-      }
-      const bf16x8 pf0 = M::from_acc<0>(s[qb]), pf1 = M::from_acc<1>(s[qb]);
-      const bf16x8 sf0 = M::from_acc<0>(dp[qb]), sf1 = M::from_acc<1>(dp[qb]);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          dv[db] = M::mma(h ? pf1 : pf0, ofr[h][db], dv[db]);
-          dk[db] = M::mma(h ? sf1 : sf0, qfr[h][db], dk[db]);
-        }
+      for (int i = 0; i < M1; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase 2.
+    dma(1);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      bf16x8 qa[KC], oa[KC];
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        qa[c] = as_bf16x8(lds_load16(QB, fo.nat(c)));
+        oa[c] = as_bf16x8(lds_load16(OB, fo.nat(c)));
+      }
+      stats(lse, delta, 1, g, LB, DB_);
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        sB = M::mma(qa[c], kf[c], sB);
+        pB = M::mma(oa[c], vf[c], pB);
+      }
+      softmax<need_mask>(sA, pA, LA, DA, lbs, 0, q0, key, g, T, right, c2, pfA, sfA);
+#pragma unroll
+      for (int i = 0; i < NPRE; ++i) {
+        const int h = i / DB, db = i - h * DB;
+        ofA[i] = lds_tr_frag(Os + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+        qfA[i] = lds_tr_frag(Qs + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
+#pragma unroll
+      for (int i = 0; i < M1; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedVALU, 8, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase 3.
+    dma(2);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+#pragma unroll
+      for (int i = NPRE; i < NTR; ++i) {
+        const int h = i / DB, db = i - h * DB;
+        ofA[i] = lds_tr_frag(Os + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+        qfA[i] = lds_tr_frag(Qs + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+      }
+#pragma unroll
+      for (int i = 0; i < NPRE; ++i) {
+        const int h = i / DB, db = i - h * DB;
+        ofB[i] = lds_tr_frag(OB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+        qfB[i] = lds_tr_frag(QB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+      }
+#pragma unroll
+      for (int i = 0; i < NTR; ++i) {
+        const int h = i / DB, db = i - h * DB;
+        dv[db] = M::mma(pfA[h], ofA[i], dv[db]);
+        dk[db] = M::mma(sfA[h], qfA[i], dk[db]);
+      }
+      softmax<need_mask>(sB, pB, LB, DB_, lbs, 1, q0, key, g, T, right, c2, pfB, sfB);
+#pragma unroll
+      for (int i = 0; i < M2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedVALU, 8, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase 4.
+    dma(3);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+#pragma unroll
+      for (int i = NPRE; i < NTR; ++i) {
+        const int h = i / DB, db = i - h * DB;
+        ofB[i] = lds_tr_frag(OB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+        qfB[i] = lds_tr_frag(QB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
+      }
+#pragma unroll
+      for (int i = 0; i < NTR; ++i) {
+        const int h = i / DB, db = i - h * DB;
+        dv[db] = M::mma(pfB[h], ofB[i], dv[db]);
+        dk[db] = M::mma(sfB[h], qfB[i], dk[db]);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
+#pragma unroll
+      for (int i = 0; i < M2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 };
 
@@ -158,6 +260,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
   __shared__ __attribute__((aligned(16))) float s_delta[2][BQ];
   __shared__ __attribute__((aligned(16))) int s_lb[2][BQ];
+  __shared__ __attribute__((aligned(8))) int s_lbmm[2][2];  // per slot: min, max of s_lb
   constexpr int kVisTiles = 256;  // query tiles whose visibility is tabulated in LDS
   __shared__ unsigned char s_vis[kVisTiles];
 
@@ -247,20 +350,35 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   DmaPlan<D, BQ> plan;
   plan.init(wave, lane, qpitch);
   float st_lse = 0.0f, st_delta = 0.0f;
-  int st_q = 0, st_pos = 0;
+  int st_q = 0, st_pos = 0, st_lbmin = 0, st_lbmax = 0;
   const float c2 = a.scale_log2;
 
   // Starts loading step st: Q and dO tiles by DMA into buf, the row
   // statistics and positions into registers.  publish() consumes them after
   // the step's compute, so no wait on these loads sits in front of it.
+  // The next tile's Q and dO loads: descriptors set by issue(), loads issued
+  // a quarter at a time by the step body (dma_part), without a branch so the
+  // body stays one straight line.  With no next step the descriptors have no
+  // records and the loads write zeros into the idle buffer.
+  u32x4s nx_q = {0u, 0u, 0u, 0u}, nx_o = {0u, 0u, 0u, 0u};
+  uint32_t nx_at = 0;
+  static_assert(DmaPlan<D, BQ>::kPerWave <= 4, "dma_part(0..3) must cover every load of a tile");
+  auto dma_part = [&](int k) {
+    plan.issue_one(nx_q, nx_at, wave, k);
+    plan.issue_one(nx_o, nx_at + C::kTileBytes, wave, k);
+  };
+  auto no_issue = [&](char* buf) {
+    nx_at = lds_addr(buf);
+    nx_q = buffer_words(a.Q, 0);
+    nx_o = buffer_words(a.dO, 0);
+  };
   auto issue = [&](Step st, char* buf) {
     const int h = kvh * a.group + st.h;
     const int q0 = (qt_begin + st.t) * BQ;
     const int64_t hoff = (((int64_t)b * T * a.H + h) * D) * 2;
-    const uint32_t at = lds_addr(buf);
-    plan.issue(tile_words(static_cast<const char*>(a.Q) + hoff, qrec, (int64_t)q0 * qpitch), at, wave);
-    plan.issue(tile_words(static_cast<const char*>(a.dO) + hoff, qrec, (int64_t)q0 * qpitch), at + C::kTileBytes,
-               wave);
+    nx_at = lds_addr(buf);
+    nx_q = tile_words(static_cast<const char*>(a.Q) + hoff, qrec, (int64_t)q0 * qpitch);
+    nx_o = tile_words(static_cast<const char*>(a.dO) + hoff, qrec, (int64_t)q0 * qpitch);
     if (tid < BQ) {
       const int qq = q0 + tid;
       const int64_t si = ((int64_t)b * a.H + h) * T + qq;
@@ -268,6 +386,25 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       st_lse = qq < T ? a.lse2[si] : INFINITY;
       st_delta = qq < T ? a.delta[si] : 0.0f;
       st_pos = (pos != nullptr && qq < T) ? pos[qq] : 0;
+    }
+    if (tid == 0) {
+      // Key lower bounds are monotone in the query without positions; with
+      // positions the bounds kernel tabulated them per 32-query chunk
+      // (queries at or beyond T count as T in both).
+      if (clb != nullptr) {
+        const int c0 = q0 / 32;
+        st_lbmin = clb[2 * c0];
+        st_lbmax = clb[2 * c0 + 1];
+#pragma unroll
+        for (int c = 1; c < BQ / 32; ++c) {
+          const bool in = c0 + c < nchunks;
+          st_lbmin = min(st_lbmin, in ? clb[2 * (c0 + c)] : T);
+          st_lbmax = max(st_lbmax, in ? clb[2 * (c0 + c) + 1] : T);
+        }
+      } else {
+        st_lbmin = key_lb(q0, T, a.left, nullptr);
+        st_lbmax = key_lb(q0 + BQ - 1, T, a.left, nullptr);
+      }
     }
   };
   auto publish = [&](int slot) {
@@ -278,29 +415,37 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       if (st_q < T) lb = max(0, max(st_q - a.left, pos != nullptr ? st_q - st_pos : 0));
       s_lb[slot][tid] = lb;
     }
+    if (tid == 0) {
+      s_lbmm[slot][0] = st_lbmin;
+      s_lbmm[slot][1] = st_lbmax;
+    }
   };
   auto compute = [&](Step st, const char* buf, int slot) {
     const int q0 = (qt_begin + st.t) * BQ;
-    DkdvStep<D>::run(buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], kf, vf, dk, dv, fo, q0, key,
-                     kw0, kw1, g, lane, T, a.right, c2);
+    DkdvStep<D>::run(dma_part, buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], s_lbmm[slot], kf, vf, dk, dv,
+                     fo, q0, key, kw0, kw1, g, T, a.right, c2);
   };
 
   const int G = t_first < n_qt_tiles ? a.group : 0;  // no visible tile: no step
   Step st{0, t_first};
   if (st.h < G) {
     issue(st, bufA);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dma_part(k);
     publish(0);
   }
   dma_wait_barrier();
   while (st.h < G) {
     const Step st1 = advance(st);
     if (st1.h < G) issue(st1, bufB);
+    else no_issue(bufB);
     compute(st, bufA, 0);
     if (st1.h < G) publish(1);
     dma_wait_barrier();
     if (st1.h >= G) break;
     const Step st2 = advance(st1);
     if (st2.h < G) issue(st2, bufA);
+    else no_issue(bufA);
     compute(st1, bufB, 1);
     if (st2.h < G) publish(0);
     dma_wait_barrier();

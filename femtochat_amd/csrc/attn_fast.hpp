@@ -206,11 +206,14 @@ struct DmaPlan {
   // Issues this wave's share of one tile's loads into the LDS tile at lds_addr.
   __device__ inline void issue(u32x4s words, uint32_t lds_addr, int wave) const {
 #pragma unroll
-    for (int j = 0; j < kPerWave; ++j) {
-      const int i = wave + kWaves * j;
-      if (kInstr % kWaves == 0 || i < kInstr)
-        dma_load16(words, goff[j], __builtin_amdgcn_readfirstlane(lds_addr + 1024 * i));
-    }
+    for (int j = 0; j < kPerWave; ++j) issue_one(words, lds_addr, wave, j);
+  }
+  // The j-th of them, for callers that spread the loads over their compute;
+  // j >= kPerWave issues nothing.
+  __device__ inline void issue_one(u32x4s words, uint32_t lds_addr, int wave, int j) const {
+    const int i = wave + kWaves * j;
+    if (j < kPerWave && (kInstr % kWaves == 0 || i < kInstr))
+      dma_load16(words, goff[j], __builtin_amdgcn_readfirstlane(lds_addr + 1024 * i));
   }
 };
 

@@ -26,7 +26,7 @@ namespace fc {
 template <int D>
 struct DkdvFastCfg {
   static constexpr int kBK = 128;  // keys per workgroup
-  static constexpr int kBQ = 64;   // queries per step
+  static constexpr int kBQ = 128;  // queries per step
   static constexpr int kKC = D / 16;
   static constexpr int kDB = D < 32 ? 1 : D / 32;
   static constexpr int kTileBytes = kBQ * 2 * D;
@@ -34,30 +34,46 @@ struct DkdvFastCfg {
 };
 
 // One step of the dK/dV kernel: the wave's 32 keys against one staged tile
-// of BQ queries, processed 32 queries at a time.
+// of BQ queries, processed as NQB blocks of 32 queries.
+//
+// The body is a pipeline over the blocks.  Phase i holds the S, dP products
+// of block i, the softmax of block i-1 and the dV, dK products of block i-2,
+// so every softmax runs under MFMAs of other blocks: at one wave per SIMD a
+// VALU instruction only overlaps an MFMA when it sits between MFMAs in the
+// wave's own instruction stream, and sched_group_barrier interleaves them
+// (plus the LDS reads) within each phase.  LDS fragments are requested a
+// phase, or a few products, before their use.
 template <int D>
 struct DkdvStep {
   using C = DkdvFastCfg<D>;
   using M = Mma<bf16>;
   static constexpr int BQ = C::kBQ, KC = C::kKC, DB = C::kDB, NQB = BQ / 32;
+  static constexpr int NPH = NQB + 2;            // phases of the body
+  static constexpr int NTR = 2 * DB;             // transposed fragments per operand and block
+  static constexpr int NPRE = NTR < 2 ? NTR : 2;  // of them requested one phase early
+  static constexpr int kSchedVALU = 0x2, kSchedMFMA = 0x8, kSchedDSRead = 0x100;
 
-  // dma(k), k = 0..3, issues a quarter of the next tile's loads; the body
+  // dma(k), k = 0..NPH-1, issues a share of the next tile's loads; the body
   // calls it at its phase boundaries so the loads queue behind the products
   // instead of all at once.
   template <typename Dma>
   __device__ static inline void run(const Dma& dma, const char* Qs, const char* Os, const float* lse,
-                                    const float* delta,
-                                    const int* lbs, const int* lbmm, const bf16x8* kf, const bf16x8* vf,
-                                    f32x16* dk, f32x16* dv, const FragOffsets<D>& fo, int q0, int key, int kw0,
-                                    int kw1, int g, int T, int right, float c2) {
-    // Smallest and largest key lower bound over the tile's queries, tabulated
-    // when the tile was published (no cross-lane reduction in the step).
-    const int lbmin = lbmm[0], lbmax = lbmm[1];
+                                    const float* delta, const int* lbs, const int* lbc, const bf16x8* kf,
+                                    const bf16x8* vf, f32x16* dk, f32x16* dv, const FragOffsets<D>& fo, int q0,
+                                    int key, int kw0, int kw1, int g, int T, int right, float c2) {
+    // Smallest and largest key lower bound over the tile's queries, from the
+    // per-chunk bounds published with the tile (no cross-lane reduction).
+    int lbmin = lbc[0], lbmax = lbc[NQB];
+#pragma unroll
+    for (int c = 1; c < NQB; ++c) {
+      lbmin = min(lbmin, lbc[c]);
+      lbmax = max(lbmax, lbc[NQB + c]);
+    }
     const int ubmin = q0 + BQ - 1 >= T ? -1 : key_ub(q0, T, right);  // ub is monotone in q
     const int ubmax = key_ub(min(q0 + BQ - 1, T - 1), T, right);
     if (lbmin > kw1 || ubmax < kw0) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) dma(k);
+      for (int k = 0; k < NPH; ++k) dma(k);
       return;
     }
     // Two straight-line bodies: tiles inside every window skip the mask.
@@ -67,36 +83,49 @@ struct DkdvStep {
       body<true>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
   }
 
-  // Step body as four phases over the tile's two 32-query blocks A and B:
-  //   1. S, dP of A
-  //   2. S, dP of B      + softmax of A
-  //   3. dV, dK from A   + softmax of B
-  //   4. dV, dK from B
-  // At one wave per SIMD, a VALU instruction only overlaps an MFMA when it
-  // sits between MFMAs in the wave's own instruction stream, so each phase
-  // interleaves one MFMA with a few VALU and LDS instructions
-  // (sched_group_barrier), and each block's softmax runs under the products
-  // of the other block.  LDS fragments are requested a phase or a few
-  // products before their use.
-  template <bool need_mask>
-  __device__ static inline void softmax(f32x16& s, f32x16& dp, const f32x4* L, const f32x4* Dl, const int* lbs,
-                                        int qb, int q0, int key, int g, int T, int right, float c2, bf16x8* pf,
-                                        bf16x8* sf) {
+  __device__ static inline void stats(const float* lse, const float* delta, int qb, int g, f32x4* L, f32x4* Dl) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i0 = 32 * qb + 8 * j + 4 * g;
+      L[j] = *reinterpret_cast<const f32x4*>(&lse[i0]);
+      Dl[j] = *reinterpret_cast<const f32x4*>(&delta[i0]);
+    }
+  }
+  // Key lower bounds of the block's rows, and a factor 0 on rows with a
+  // single visible key (whose dS is zero), else 1.
+  __device__ static inline void bounds(const int* lbs, int qb, int g, i32x4* LB, f32x4* Z) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i0 = 32 * qb + 8 * j + 4 * g;
+      LB[j] = *reinterpret_cast<const i32x4*>(&lbs[i0]);
+      Z[j] = *reinterpret_cast<const f32x4*>(&lbs[BQ + i0]);
+    }
+  }
+
+  // P = exp2(S c2 - lse2), dS = P (dP - Delta), both rounded to bf16 as the
+  // operands of dV += P^T dO and dK += dS^T Q.
+  // The mask (need_mask) is branch-free: P is zero unless key >= lb(q) and
+  // key - q <= right, dS = P (dP - Delta) z(q) with z = 0 on rows with a single
+  // visible key.  Rows at or beyond T have lse2 = +inf, so P and dS vanish
+  // there without a test.
+  template <bool need_mask>
+  __device__ static inline void softmax(f32x16& s, f32x16& dp, const f32x4* L, const f32x4* Dl, const i32x4* LB,
+                                        const f32x4* Z, int qb, int q0, int key, int g, int right, float c2,
+                                        bf16x8* pf, bf16x8* sf) {
+    // key - q <= right  <=>  x >= -(8j + t) for row 4g + 8j + t.
+    const int x = q0 + 32 * qb + 4 * g - key + right;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int r = 4 * j + t;
         float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -L[j][t]));
-        float ds = p * (dp[r] - Dl[j][t]);
         if (need_mask) {
-          const int lbq = lbs[i0 + t];
-          const int ubq = key_ub(q0 + i0 + t, T, right);
-          const bool vis = key >= lbq && key <= ubq;
-          p = vis ? p : 0.0f;
-          ds = (vis && ubq > lbq) ? ds : 0.0f;
+          p = x >= -(8 * j + t) ? p : 0.0f;
+          p = key >= LB[j][t] ? p : 0.0f;
         }
+        float ds = p * (dp[r] - Dl[j][t]);
+        if (need_mask) ds *= Z[j][t];
         s[r] = p;
         dp[r] = ds;
       }
@@ -107,145 +136,87 @@ struct DkdvStep {
     sf[1] = M::from_acc<1>(dp);
   }
 
-  static constexpr int kSchedVALU = 0x2, kSchedMFMA = 0x8, kSchedDSRead = 0x100;
-  static constexpr int NTR = 2 * DB;  // transposed fragments per operand and block
-  static constexpr int NPRE = NTR < 2 ? NTR : 2;  // of them requested one phase early
-
-  __device__ static inline void stats(const float* lse, const float* delta, int qb, int g, f32x4* L, f32x4* Dl) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i0 = 32 * qb + 8 * j + 4 * g;
-      L[j] = *reinterpret_cast<const f32x4*>(&lse[i0]);
-      Dl[j] = *reinterpret_cast<const f32x4*>(&delta[i0]);
-    }
+  __device__ static inline bf16x8 trq(const char* tile, int qb, int i, const FragOffsets<D>& fo) {
+    const int h = i / DB, db = i - h * DB;
+    return lds_tr_frag(tile + (32 * qb + 16 * h) * 2 * D, fo.tr(0, db), fo.tr(1, db));
   }
 
   template <bool need_mask, typename Dma>
   __device__ static inline void body(const Dma& dma, const char* Qs, const char* Os, const float* lse,
-                                     const float* delta,
-                                     const int* lbs, const bf16x8* kf, const bf16x8* vf, f32x16* dk, f32x16* dv,
-                                     const FragOffsets<D>& fo, int q0, int key, int g, int T, int right, float c2) {
-    static_assert(NQB == 2, "the phase schedule assumes two 32-query blocks per tile");
+                                     const float* delta, const int* lbs, const bf16x8* kf, const bf16x8* vf,
+                                     f32x16* dk, f32x16* dv, const FragOffsets<D>& fo, int q0, int key, int g,
+                                     int T, int right, float c2) {
     constexpr int M1 = 2 * KC;   // MFMAs of S, dP per block
     constexpr int M2 = 2 * NTR;  // MFMAs of dV, dK per block
-    const char* QB = Qs + 32 * 2 * D;
-    const char* OB = Os + 32 * 2 * D;
-    f32x16 sA = zero16(), pA = zero16(), sB = zero16(), pB = zero16();
-    f32x4 LA[4], DA[4], LB[4], DB_[4];
-    bf16x8 pfA[2], sfA[2], pfB[2], sfB[2];
-    bf16x8 ofA[NTR], qfA[NTR], ofB[NTR], qfB[NTR];  // index h * DB + db
-
-    // Phase 1.
-    dma(0);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-      bf16x8 qa[KC], oa[KC];
+    f32x16 s[NQB], dp[NQB];
+    f32x4 L[NQB][4], Dl[NQB][4];
+    i32x4 LB[NQB][4];
+    f32x4 Z[NQB][4];
+    bf16x8 pf[NQB][2], sf[NQB][2];
+    bf16x8 ofr[NQB][NTR], qfr[NQB][NTR];  // index h * DB + db
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        qa[c] = as_bf16x8(lds_load16(Qs, fo.nat(c)));
-        oa[c] = as_bf16x8(lds_load16(Os, fo.nat(c)));
-      }
-      stats(lse, delta, 0, g, LA, DA);
+    for (int ph = 0; ph < NPH; ++ph) {
+      const int b1 = ph, bs = ph - 1, b2 = ph - 2;  // blocks of the three stages
+      dma(ph);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b1 < NQB) {
+        const char* qt = Qs + 32 * b1 * 2 * D;
+        const char* ot = Os + 32 * b1 * 2 * D;
+        bf16x8 qa[KC], oa[KC];
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        sA = M::mma(qa[c], kf[c], sA);
-        pA = M::mma(oa[c], vf[c], pA);
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 6, 0);
+        for (int c = 0; c < KC; ++c) {
+          qa[c] = as_bf16x8(lds_load16(qt, fo.nat(c)));
+          oa[c] = as_bf16x8(lds_load16(ot, fo.nat(c)));
+        }
+        stats(lse, delta, b1, g, L[b1], Dl[b1]);
+        if (need_mask) bounds(lbs, b1, g, LB[b1], Z[b1]);
+        s[b1] = zero16();
+        dp[b1] = zero16();
 #pragma unroll
-      for (int i = 0; i < M1; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+        for (int c = 0; c < KC; ++c) {
+          s[b1] = M::mma(qa[c], kf[c], s[b1]);
+          dp[b1] = M::mma(oa[c], vf[c], dp[b1]);
+        }
       }
+      if (b2 >= 0) {
+#pragma unroll
+        for (int i = NPRE; i < NTR; ++i) {
+          ofr[b2][i] = trq(Os, b2, i, fo);
+          qfr[b2][i] = trq(Qs, b2, i, fo);
+        }
+#pragma unroll
+        for (int i = 0; i < NTR; ++i) {
+          const int h = i / DB, db = i - h * DB;
+          dv[db] = M::mma(pf[b2][h], ofr[b2][i], dv[db]);
+          dk[db] = M::mma(sf[b2][h], qfr[b2][i], dk[db]);
+        }
+      }
+      if (bs >= 0 && bs < NQB) {
+        softmax<need_mask>(s[bs], dp[bs], L[bs], Dl[bs], LB[bs], Z[bs], bs, q0, key, g, right, c2, pf[bs],
+                           sf[bs]);
+        // First transposed fragments of the block, for the next phase.
+#pragma unroll
+        for (int i = 0; i < NPRE; ++i) {
+          ofr[bs][i] = trq(Os, bs, i, fo);
+          qfr[bs][i] = trq(Qs, bs, i, fo);
+        }
+      }
+      // Interleave: one MFMA, a few LDS reads, a few VALU instructions.
+      const int nmf = (b1 < NQB ? M1 : 0) + (b2 >= 0 ? M2 : 0);
+      const bool valu = bs >= 0 && bs < NQB;
+      if (ph == 0) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 6, 0);
+      else __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * (M1 > M2 ? M1 : M2); ++i) {
+        if (i < nmf) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+          if (valu && nmf > 16) __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4, 0);
+          if (valu && nmf <= 16) __builtin_amdgcn_sched_group_barrier(kSchedVALU, 8, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // Phase 2.
-    dma(1);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-      bf16x8 qa[KC], oa[KC];
-#pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        qa[c] = as_bf16x8(lds_load16(QB, fo.nat(c)));
-        oa[c] = as_bf16x8(lds_load16(OB, fo.nat(c)));
-      }
-      stats(lse, delta, 1, g, LB, DB_);
-#pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        sB = M::mma(qa[c], kf[c], sB);
-        pB = M::mma(oa[c], vf[c], pB);
-      }
-      softmax<need_mask>(sA, pA, LA, DA, lbs, 0, q0, key, g, T, right, c2, pfA, sfA);
-#pragma unroll
-      for (int i = 0; i < NPRE; ++i) {
-        const int h = i / DB, db = i - h * DB;
-        ofA[i] = lds_tr_frag(Os + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-        qfA[i] = lds_tr_frag(Qs + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
-#pragma unroll
-      for (int i = 0; i < M1; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedVALU, 8, 0);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Phase 3.
-    dma(2);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-#pragma unroll
-      for (int i = NPRE; i < NTR; ++i) {
-        const int h = i / DB, db = i - h * DB;
-        ofA[i] = lds_tr_frag(Os + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-        qfA[i] = lds_tr_frag(Qs + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-      }
-#pragma unroll
-      for (int i = 0; i < NPRE; ++i) {
-        const int h = i / DB, db = i - h * DB;
-        ofB[i] = lds_tr_frag(OB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-        qfB[i] = lds_tr_frag(QB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-      }
-#pragma unroll
-      for (int i = 0; i < NTR; ++i) {
-        const int h = i / DB, db = i - h * DB;
-        dv[db] = M::mma(pfA[h], ofA[i], dv[db]);
-        dk[db] = M::mma(sfA[h], qfA[i], dk[db]);
-      }
-      softmax<need_mask>(sB, pB, LB, DB_, lbs, 1, q0, key, g, T, right, c2, pfB, sfB);
-#pragma unroll
-      for (int i = 0; i < M2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedVALU, 8, 0);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Phase 4.
-    dma(3);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-#pragma unroll
-      for (int i = NPRE; i < NTR; ++i) {
-        const int h = i / DB, db = i - h * DB;
-        ofB[i] = lds_tr_frag(OB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-        qfB[i] = lds_tr_frag(QB + 16 * h * 2 * D, fo.tr(0, db), fo.tr(1, db));
-      }
-#pragma unroll
-      for (int i = 0; i < NTR; ++i) {
-        const int h = i / DB, db = i - h * DB;
-        dv[db] = M::mma(pfB[h], ofB[i], dv[db]);
-        dk[db] = M::mma(sfB[h], qfB[i], dk[db]);
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
-#pragma unroll
-      for (int i = 0; i < M2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
   }
 };
 
@@ -259,8 +230,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   __shared__ __attribute__((aligned(1024))) char bufB[C::kStageBytes];
   __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
   __shared__ __attribute__((aligned(16))) float s_delta[2][BQ];
-  __shared__ __attribute__((aligned(16))) int s_lb[2][BQ];
-  __shared__ __attribute__((aligned(8))) int s_lbmm[2][2];  // per slot: min, max of s_lb
+  __shared__ __attribute__((aligned(16))) int s_lb[2][2 * BQ];  // per slot: lb, then z as float (see softmax)
+  __shared__ __attribute__((aligned(16))) int s_lbc[2][2][BQ / 32];  // per slot: chunk min, max of s_lb
   constexpr int kVisTiles = 256;  // query tiles whose visibility is tabulated in LDS
   __shared__ unsigned char s_vis[kVisTiles];
 
@@ -350,22 +321,26 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   DmaPlan<D, BQ> plan;
   plan.init(wave, lane, qpitch);
   float st_lse = 0.0f, st_delta = 0.0f;
-  int st_q = 0, st_pos = 0, st_lbmin = 0, st_lbmax = 0;
+  int st_q = 0, st_pos = 0, st_cmin = 0, st_cmax = 0;
   const float c2 = a.scale_log2;
 
-  // Starts loading step st: Q and dO tiles by DMA into buf, the row
-  // statistics and positions into registers.  publish() consumes them after
-  // the step's compute, so no wait on these loads sits in front of it.
+  // issue() starts loading step st: the row statistics, positions and chunk
+  // bounds into registers, each load unconditional (clamped index, or a
+  // stand-in array when there are no positions) so that no wait for it is
+  // needed before publish(), which consumes them after the step's compute.
   // The next tile's Q and dO loads: descriptors set by issue(), loads issued
   // a quarter at a time by the step body (dma_part), without a branch so the
   // body stays one straight line.  With no next step the descriptors have no
   // records and the loads write zeros into the idle buffer.
   u32x4s nx_q = {0u, 0u, 0u, 0u}, nx_o = {0u, 0u, 0u, 0u};
   uint32_t nx_at = 0;
-  static_assert(DmaPlan<D, BQ>::kPerWave <= 4, "dma_part(0..3) must cover every load of a tile");
+  constexpr int NPH = DkdvStep<D>::NPH;
   auto dma_part = [&](int k) {
-    plan.issue_one(nx_q, nx_at, wave, k);
-    plan.issue_one(nx_o, nx_at + C::kTileBytes, wave, k);
+#pragma unroll
+    for (int j = k; j < DmaPlan<D, BQ>::kPerWave; j += NPH) {
+      plan.issue_one(nx_q, nx_at, wave, j);
+      plan.issue_one(nx_o, nx_at + C::kTileBytes, wave, j);
+    }
   };
   auto no_issue = [&](char* buf) {
     nx_at = lds_addr(buf);
@@ -379,50 +354,51 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
     nx_at = lds_addr(buf);
     nx_q = tile_words(static_cast<const char*>(a.Q) + hoff, qrec, (int64_t)q0 * qpitch);
     nx_o = tile_words(static_cast<const char*>(a.dO) + hoff, qrec, (int64_t)q0 * qpitch);
+    const int64_t srow = ((int64_t)b * a.H + h) * T;
+    const int32_t* stand_in = reinterpret_cast<const int32_t*>(a.delta + srow);  // T readable words
     if (tid < BQ) {
       const int qq = q0 + tid;
-      const int64_t si = ((int64_t)b * a.H + h) * T + qq;
+      const int qc = min(qq, T - 1);
       st_q = qq;
-      st_lse = qq < T ? a.lse2[si] : INFINITY;
-      st_delta = qq < T ? a.delta[si] : 0.0f;
-      st_pos = (pos != nullptr && qq < T) ? pos[qq] : 0;
+      st_lse = a.lse2[srow + qc];
+      st_delta = a.delta[srow + qc];
+      st_pos = (pos != nullptr ? pos : stand_in)[qc];
     }
-    if (tid == 0) {
-      // Key lower bounds are monotone in the query without positions; with
-      // positions the bounds kernel tabulated them per 32-query chunk
-      // (queries at or beyond T count as T in both).
-      if (clb != nullptr) {
-        const int c0 = q0 / 32;
-        st_lbmin = clb[2 * c0];
-        st_lbmax = clb[2 * c0 + 1];
-#pragma unroll
-        for (int c = 1; c < BQ / 32; ++c) {
-          const bool in = c0 + c < nchunks;
-          st_lbmin = min(st_lbmin, in ? clb[2 * (c0 + c)] : T);
-          st_lbmax = max(st_lbmax, in ? clb[2 * (c0 + c) + 1] : T);
-        }
-      } else {
-        st_lbmin = key_lb(q0, T, a.left, nullptr);
-        st_lbmax = key_lb(q0 + BQ - 1, T, a.left, nullptr);
-      }
+    if (tid < BQ / 32) {
+      // The bounds kernel's per-chunk (min, max) key lower bound.
+      const int c = min(q0 / 32 + tid, nchunks - 1);
+      const int32_t* cb = clb != nullptr ? clb + 2 * c : stand_in;
+      st_cmin = cb[0];
+      st_cmax = cb[clb != nullptr ? 1 : 0];
     }
   };
   auto publish = [&](int slot) {
     if (tid < BQ) {
-      s_lse[slot][tid] = st_lse;
-      s_delta[slot][tid] = st_delta;
+      const bool in = st_q < T;
+      s_lse[slot][tid] = in ? st_lse : INFINITY;
+      s_delta[slot][tid] = in ? st_delta : 0.0f;
       int lb = T;
-      if (st_q < T) lb = max(0, max(st_q - a.left, pos != nullptr ? st_q - st_pos : 0));
+      if (in) lb = max(0, max(st_q - a.left, pos != nullptr ? st_q - st_pos : 0));
       s_lb[slot][tid] = lb;
+      s_lb[slot][BQ + tid] = __builtin_bit_cast(int, key_ub(st_q, T, a.right) > lb ? 1.0f : 0.0f);
     }
-    if (tid == 0) {
-      s_lbmm[slot][0] = st_lbmin;
-      s_lbmm[slot][1] = st_lbmax;
+    if (tid < BQ / 32) {
+      // Key lower bounds of chunk tid of the tile (queries at or beyond T
+      // count as T): monotone in the query without positions, tabulated per
+      // chunk with them.
+      const int qc0 = (st_q - tid) + 32 * tid;  // st_q is q0 + tid here
+      int lo = key_lb(qc0, T, a.left, nullptr), hi = key_lb(qc0 + 31, T, a.left, nullptr);
+      if (clb != nullptr) {
+        lo = qc0 < T ? st_cmin : T;
+        hi = qc0 < T ? st_cmax : T;
+      }
+      s_lbc[slot][0][tid] = lo;
+      s_lbc[slot][1][tid] = hi;
     }
   };
   auto compute = [&](Step st, const char* buf, int slot) {
     const int q0 = (qt_begin + st.t) * BQ;
-    DkdvStep<D>::run(dma_part, buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], s_lbmm[slot], kf, vf, dk, dv,
+    DkdvStep<D>::run(dma_part, buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], s_lbc[slot][0], kf, vf, dk, dv,
                      fo, q0, key, kw0, kw1, g, T, a.right, c2);
   };
 
@@ -431,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   if (st.h < G) {
     issue(st, bufA);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) dma_part(k);
+    for (int k = 0; k < NPH; ++k) dma_part(k);
     publish(0);
   }
   dma_wait_barrier();

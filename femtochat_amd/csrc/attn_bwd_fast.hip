@@ -334,10 +334,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   // records and the loads write zeros into the idle buffer.
   u32x4s nx_q = {0u, 0u, 0u, 0u}, nx_o = {0u, 0u, 0u, 0u};
   uint32_t nx_at = 0;
-  constexpr int NPH = DkdvStep<D>::NPH;
+  // Phases 0..3 of a step issue the loads, so they have the rest of the step
+  // to land; later phases issue none.
+  constexpr int NPH = DkdvStep<D>::NPH, NDMA = NPH < 4 ? NPH : 4;
+  constexpr int kPer = (DmaPlan<D, BQ>::kPerWave + NDMA - 1) / NDMA;
   auto dma_part = [&](int k) {
 #pragma unroll
-    for (int j = k; j < DmaPlan<D, BQ>::kPerWave; j += NPH) {
+    for (int j = k * kPer; j < (k + 1) * kPer; ++j) {
       plan.issue_one(nx_q, nx_at, wave, j);
       plan.issue_one(nx_o, nx_at + C::kTileBytes, wave, j);
     }
@@ -545,63 +548,128 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   const int kt0 = (kmin / BN) * BN;
   const int ntiles = kmax >= kmin ? (kmax - kt0) / BN + 1 : 0;
 
-  auto issue = [&](int it, char* buf) {
-    const int64_t row0 = (int64_t)(kt0 + it * BN) * kpitch;
-    const uint32_t at = lds_addr(buf);
-    plan.issue(tile_words(Kb, krec, row0), at, wave);
-    plan.issue(tile_words(Vb, krec, row0), at + C::kTileBytes, wave);
+  // The next tile's K and V loads: descriptors set by issue(), loads issued a
+  // share at a time at the phase boundaries of the tile body (dma_part),
+  // branch-free: with no next tile the descriptors have no records and the
+  // loads write zeros into the idle buffer.
+  u32x4s nx_k = {0u, 0u, 0u, 0u}, nx_v = {0u, 0u, 0u, 0u};
+  uint32_t nx_at = 0;
+  // Phases 0 and 1 of a tile issue the loads, so they have the rest of the
+  // tile to land.
+  constexpr int NPH = 4, NDMA = 2;
+  constexpr int kPer = (DmaPlan<D, BN>::kPerWave + NDMA - 1) / NDMA;
+  auto dma_part = [&](int k) {
+#pragma unroll
+    for (int j = k * kPer; j < (k + 1) * kPer; ++j) {
+      plan.issue_one(nx_k, nx_at, wave, j);
+      plan.issue_one(nx_v, nx_at + C::kTileBytes, wave, j);
+    }
   };
+  auto issue = [&](int it, char* buf) {
+    nx_at = lds_addr(buf);
+    if (it < ntiles) {
+      const int64_t row0 = (int64_t)(kt0 + it * BN) * kpitch;
+      nx_k = tile_words(Kb, krec, row0);
+      nx_v = tile_words(Vb, krec, row0);
+    } else {
+      nx_k = buffer_words(Kb, 0);
+      nx_v = buffer_words(Vb, 0);
+    }
+  };
+
+  // Tile body: a pipeline over the tile's two 32-key blocks, phase i holding
+  // S^T, dP^T of block i, the softmax of block i-1 and dQ^T += K^T dS^T of
+  // block i-2, with MFMAs, LDS reads and VALU interleaved.
+  constexpr int kSchedVALU = 0x2, kSchedMFMA = 0x8, kSchedDSRead = 0x100;
+  constexpr int M1 = 2 * KC, M2 = 2 * DB;
   auto body = [&](auto mask_tag, int kt, const char* Ks) {
     constexpr bool need_mask = decltype(mask_tag)::value;
     const char* Vs = Ks + C::kTileBytes;
+    f32x16 s[NKB], dp[NKB];
+    bf16x8 sf[NKB][2];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      f32x16 s = zero16(), dp = zero16();
+    for (int ph = 0; ph < NKB + 2; ++ph) {
+      const int b1 = ph, bs = ph - 1, b2 = ph - 2;
+      dma_part(ph);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b1 < NKB) {
+        bf16x8 ka[KC], va[KC];
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const bf16x8 kfrag = as_bf16x8(lds_load16(Ks + 32 * kb * 2 * D, fo.nat(c)));
-        const bf16x8 vfrag = as_bf16x8(lds_load16(Vs + 32 * kb * 2 * D, fo.nat(c)));
-        s = M::mma(kfrag, qf[c], s);
-        dp = M::mma(vfrag, of[c], dp);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, neg_lse));
-        float ds = p * (dp[r] - dlt);
-        if (need_mask) {
-          const int kk = kt + 32 * kb + acc_row(r, g);
-          ds = (kk >= lb && kk <= ub && multiple) ? ds : 0.0f;
+        for (int c = 0; c < KC; ++c) {
+          ka[c] = as_bf16x8(lds_load16(Ks + 32 * b1 * 2 * D, fo.nat(c)));
+          va[c] = as_bf16x8(lds_load16(Vs + 32 * b1 * 2 * D, fo.nat(c)));
         }
-        dp[r] = ds;
-      }
-      const bf16x8 sf0 = M::from_acc<0>(dp), sf1 = M::from_acc<1>(dp);
-      // dQ^T += K^T dS^T for the 2 chunks of 16 keys of this block.
+        s[b1] = zero16();
+        dp[b1] = zero16();
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const char* kchunk = Ks + 16 * (2 * kb + hh) * 2 * D;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const bf16x8 kfr = lds_tr_frag(kchunk, fo.tr(0, db), fo.tr(1, db));
-          dq[db] = M::mma(kfr, hh ? sf1 : sf0, dq[db]);
+        for (int c = 0; c < KC; ++c) {
+          s[b1] = M::mma(ka[c], qf[c], s[b1]);
+          dp[b1] = M::mma(va[c], of[c], dp[b1]);
         }
       }
+      if (b2 >= 0) {
+        // dQ^T += K^T dS^T for the block's 2 chunks of 16 keys.
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const char* kchunk = Ks + 16 * (2 * b2 + hh) * 2 * D;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const bf16x8 kfr = lds_tr_frag(kchunk, fo.tr(0, db), fo.tr(1, db));
+            dq[db] = M::mma(kfr, sf[b2][hh], dq[db]);
+          }
+        }
+      }
+      if (bs >= 0 && bs < NKB) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[bs][r], c2, neg_lse));
+          float ds = p * (dp[bs][r] - dlt);
+          if (need_mask) {
+            const int kk = kt + 32 * bs + acc_row(r, g);
+            ds = (kk >= lb) & (kk <= ub) & multiple ? ds : 0.0f;
+          }
+          dp[bs][r] = ds;
+        }
+        sf[bs][0] = M::from_acc<0>(dp[bs]);
+        sf[bs][1] = M::from_acc<1>(dp[bs]);
+      }
+      const int nmf = (b1 < NKB ? M1 : 0) + (b2 >= 0 ? M2 : 0);
+      const bool valu = bs >= 0 && bs < NKB;
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
+#pragma unroll
+      for (int i = 0; i < M1 + M2; ++i) {
+        if (i < nmf) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+          if (valu) __builtin_amdgcn_sched_group_barrier(kSchedVALU, 5, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   auto compute = [&](int it, const char* Ks) {
     const int kt = kt0 + it * BN;
-    if (wlb_min > kt + BN - 1 || wub_max < kt) return;
+    if (wlb_min > kt + BN - 1 || wub_max < kt) {
+#pragma unroll
+      for (int k = 0; k < NPH; ++k) dma_part(k);
+      return;
+    }
     if (wlb_max <= kt && kt + BN - 1 <= wub_min) body(std::false_type{}, kt, Ks);
     else body(std::true_type{}, kt, Ks);
   };
 
-  if (ntiles > 0) issue(0, bufA);
+  if (ntiles > 0) {
+    issue(0, bufA);
+#pragma unroll
+    for (int k = 0; k < NPH; ++k) dma_part(k);
+  }
   dma_wait_barrier();
   for (int it = 0; it < ntiles; it += 2) {
-    if (it + 1 < ntiles) issue(it + 1, bufB);
+    issue(it + 1, bufB);
     compute(it, bufA);
     dma_wait_barrier();
     if (it + 1 >= ntiles) break;
-    if (it + 2 < ntiles) issue(it + 2, bufA);
+    issue(it + 2, bufA);
     compute(it + 1, bufB);
     dma_wait_barrier();
   }

@@ -239,10 +239,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_kt = (T + C::kBK - 1) / C::kBK;
-  const int id = xcd_remap(blockIdx.x, n_kt * a.Hkv * a.B);
-  const int bkv = id / n_kt;
-  const int kt = id - bkv * n_kt;
-  const int b = bkv / a.Hkv, kvh = bkv - b * a.Hkv;
+  // Key tiles that the most query tiles can see come first.
+  const GridItem it0 = heavy_first(blockIdx.x, a.Hkv * a.B);
+  const int kt = it0.rank;
+  const int b = it0.row / a.Hkv, kvh = it0.row - b * a.Hkv;
   const int k0 = kt * C::kBK;
   const int k1 = min(k0 + C::kBK, T) - 1;
   const int kw0 = k0 + 32 * wave, kw1 = kw0 + 31;
@@ -491,10 +491,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_qt = (T + C::kBM - 1) / C::kBM;
-  const int id = xcd_remap(blockIdx.x, n_qt * a.H * a.B);
-  const int bh = id / n_qt;
-  const int qt = n_qt - 1 - (id - bh * n_qt);
-  const int b = bh / a.H, h = bh - b * a.H;
+  const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
+  const int qt = n_qt - 1 - it0.rank;  // longest query tiles first
+  int b, h;
+  query_row(it0.row, a.B, a.Hkv, a.group, b, h);
   const int kvh = h / a.group;
 
   const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;

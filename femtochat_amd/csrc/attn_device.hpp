@@ -152,6 +152,25 @@ __device__ inline int xcd_remap(int id, int total) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
 }
 
+// Grid order for (row, tile) work items: all rows' heaviest tiles first
+// (rank 0), then the next heaviest, and so on, so the last workgroups
+// dispatched are the lightest and no long one starts near the end.  Rows
+// are the inner index: the hardware sends workgroup id to XCD id % 8, so a
+// row count divisible by 8 keeps each row (and its K/V in L2) on one XCD.
+struct GridItem {
+  int row, rank;
+};
+__device__ inline GridItem heavy_first(int id, int rows) { return {id % rows, id / rows}; }
+
+// (batch, query head) of query-side row r, numbered KV group member outer
+// and (batch, KV head) inner: the heads that share a KV head are B*Hkv rows
+// apart, on one XCD whenever B*Hkv is divisible by 8.
+__device__ inline void query_row(int r, int B, int Hkv, int group, int& b, int& h) {
+  const int bkv = r % (B * Hkv), gi = r / (B * Hkv);
+  b = bkv / Hkv;
+  h = (bkv - b * Hkv) * group + gi;
+}
+
 // Visible key range of query q (0-based): lb <= k <= ub.  left/right are the
 // normalised window (causal -> left = T); pos is the row's positions or null.
 __device__ inline int key_lb(int q, int T, int left, const int32_t* pos) {

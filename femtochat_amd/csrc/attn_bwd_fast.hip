@@ -69,6 +69,9 @@ struct DkdvStep {
       lbmin = min(lbmin, lbc[c]);
       lbmax = max(lbmax, lbc[NQB + c]);
     }
+    // LDS broadcasts, the same on every lane: scalar branches below.
+    lbmin = __builtin_amdgcn_readfirstlane(lbmin);
+    lbmax = __builtin_amdgcn_readfirstlane(lbmax);
     const int ubmin = q0 + BQ - 1 >= T ? -1 : key_ub(q0, T, right);  // ub is monotone in q
     const int ubmax = key_ub(min(q0 + BQ - 1, T - 1), T, right);
     if (lbmin > kw1 || ubmax < kw0) {

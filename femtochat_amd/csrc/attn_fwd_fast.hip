@@ -120,6 +120,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
     wub_min = min(wub_min, wave_min32(ub[qb]));
     wub_max = max(wub_max, wave_max32(ub[qb]));
   }
+  // The reductions are the same on every lane; saying so moves the per-tile
+  // decisions below to scalar branches (as vector values the compiler made
+  // them exec-masked and copied the accumulators at every join).
+  wlb_min = __builtin_amdgcn_readfirstlane(wlb_min);
+  wlb_max = __builtin_amdgcn_readfirstlane(wlb_max);
+  wub_min = __builtin_amdgcn_readfirstlane(wub_min);
+  wub_max = __builtin_amdgcn_readfirstlane(wub_max);
   if (lane == 0) {
     s_bounds[0][wave] = wlb_min;
     s_bounds[1][wave] = wub_max;
@@ -164,6 +171,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
     kmin = min(kmin, s_bounds[0][w]);
     kmax = max(kmax, s_bounds[1][w]);
   }
+  kmin = __builtin_amdgcn_readfirstlane(kmin);
+  kmax = __builtin_amdgcn_readfirstlane(kmax);
   const int kt0 = (kmin / BN) * BN;
   const int ntiles = kmax >= kmin ? (kmax - kt0) / BN + 1 : 0;
 

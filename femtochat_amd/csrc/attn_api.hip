@@ -214,6 +214,10 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, c
   const hipStream_t s = static_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(workspace);
 
+  // Fast mode with bf16 O and dO: the dQ kernel computes the preprocess
+  // itself and runs first; otherwise a preprocess launch (which also makes
+  // the bf16 copy of an fp32 dO) precedes both kernels.
+  const bool fused_stats = p.bf16 && p.out_bf16 && p.dout_bf16;
   fc::PreArgs pa{};
   pa.dO = dO;
   pa.O = O;
@@ -227,8 +231,11 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, c
   pa.B = p.B;
   pa.dO_bf16 = p.dout_bf16 ? 1 : 0;
   pa.O_bf16 = p.out_bf16 ? 1 : 0;
-  hipError_t e = fc::launch_bwd_pre(p, pa, s);
-  if (e != hipSuccess) return fail(FC_ERR_HIP, "backward preprocess launch failed: %s", hipGetErrorString(e));
+  hipError_t e = hipSuccess;
+  if (!fused_stats) {
+    e = fc::launch_bwd_pre(p, pa, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "backward preprocess launch failed: %s", hipGetErrorString(e));
+  }
 
   int32_t* chunk_lb = nullptr;
   if (p.positions) {
@@ -261,6 +268,19 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, c
   a.accumulate = p.accumulate ? 1 : 0;
   a.scale = (float)(1.0 / std::sqrt((double)p.D));
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)p.D));
+  if (fused_stats) {
+    a.stats = 1;
+    a.O = O;
+    a.l = l;
+    a.m = m;
+    a.delta_out = pa.delta;
+    a.lse2_out = pa.lse2;
+    e = fc::launch_bwd_dq(p, a, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "dQ launch failed: %s", hipGetErrorString(e));
+    e = fc::launch_bwd_dkdv(p, a, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "dK/dV launch failed: %s", hipGetErrorString(e));
+    return ok();
+  }
   e = fc::launch_bwd_dkdv(p, a, s);
   if (e != hipSuccess) return fail(FC_ERR_HIP, "dK/dV launch failed: %s", hipGetErrorString(e));
   e = fc::launch_bwd_dq(p, a, s);

@@ -518,19 +518,43 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
     s_bounds[1][wave] = wub_max;
   }
   const int64_t si = ((int64_t)b * a.H + h) * T + q;
-  const float neg_lse = q < T ? -a.lse2[si] : -INFINITY;
-  const float dlt = q < T ? a.delta[si] : 0.0f;
 
   bf16x8 qf[KC], of[KC];
+  const int qoff = q * qpitch + 16 * g;
   {
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(static_cast<const char*>(a.Q) + hoff, (uint32_t)qrec);
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<const char*>(a.dO) + hoff, (uint32_t)qrec);
-    const int qoff = q * qpitch + 16 * g;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       qf[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c, 0));
       of[c] = as_bf16x8(buf_load16(ro, qoff + 32 * c, 0));
     }
+  }
+  float neg_lse, dlt;
+  if (a.stats) {
+    // The backward preprocess for this workgroup's queries (the sum over D
+    // is split between the two half-waves, which hold alternate 8-element
+    // runs of the head dimension), written out for the dK/dV kernel.
+    const __amdgpu_buffer_rsrc_t rO = make_rsrc(static_cast<const char*>(a.O) + hoff, (uint32_t)qrec);
+    float part = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const bf16x8 ov = as_bf16x8(buf_load16(rO, qoff + 32 * c, 0));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += static_cast<float>(of[c][e]) * static_cast<float>(ov[e]);
+    }
+    dlt = part + __shfl_xor(part, 32);
+    float lse2 = INFINITY;
+    if (q < T) lse2 = a.m[si] * kLog2e + __builtin_amdgcn_logf(fmaxf(a.l[si], kFltEps));
+    if (q < T && g == 0) {
+      a.delta_out[si] = dlt;
+      a.lse2_out[si] = lse2;
+    }
+    neg_lse = -lse2;
+    dlt = q < T ? dlt : 0.0f;
+  } else {
+    neg_lse = q < T ? -a.lse2[si] : -INFINITY;
+    dlt = q < T ? a.delta[si] : 0.0f;
   }
   FragOffsets<D> fo;
   fo.init(lane);

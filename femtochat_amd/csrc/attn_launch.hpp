@@ -59,6 +59,15 @@ struct BwdArgs {
   const void* V;
   const float* delta;
   const float* lse2;
+  // stats != 0 (fast mode, bf16 O and dO): the dQ kernel computes Delta and
+  // lse2 itself from O, dO, l, m and writes them to delta_out/lse2_out for
+  // the dK/dV kernel, which then runs after it (no preprocess launch).
+  int stats;
+  const void* O;
+  const float* l;
+  const float* m;
+  float* delta_out;
+  float* lse2_out;
   const int32_t* pos;
   const int32_t* chunk_lb;
   void* dQ;

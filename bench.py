@@ -96,6 +96,55 @@ def cpu_baseline(wl, rows: int, threads: int) -> dict:
     }
 
 
+def measure_prologue(wl, dev, steps: int) -> dict:
+    """The attention prologue (rotary embedding + RMS norm x 1.2) on the
+    workload's Q and K, forward and backward (overwrite), bf16: HBM-bound, so
+    its roofline is algorithmic bytes (X read, Y written; dY and X read, dX
+    written) per unit time against 8 TB/s.  Not part of the headline value."""
+    import torch
+
+    import femtochat_amd._lib as L
+    from femtochat_amd import attention_prologue_, delta_attention_prologue_, rotary_embeddings
+
+    sin, cos = rotary_embeddings(wl.T, wl.D, device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    Xs = [torch.randn(wl.B, wl.T, nh, wl.D, device=dev, generator=g).to(torch.bfloat16) for nh in (wl.H, wl.Hkv)]
+    Ys = [torch.empty_like(x) for x in Xs]
+    dXs = [torch.empty_like(x) for x in Xs]
+
+    def once():
+        for X, Y in zip(Xs, Ys):
+            attention_prologue_(Y, X, (sin, cos))
+        for X, Y, dX in zip(Xs, Ys, dXs):
+            delta_attention_prologue_(dX, Y, X, (sin, cos), accumulate=False)
+
+    for _ in range(3):
+        once()
+    torch.cuda.synchronize()
+    L.profile_collect()
+    L.profile_enable(True)
+    for _ in range(steps):
+        once()
+    torch.cuda.synchronize()
+    L.profile_enable(False)
+    k = L.profile_collect()
+    nbytes = sum(x.numel() * x.element_size() for x in Xs)
+    out = {"workload": f"{wl.name} Q (B,T,H,D) and K (B,T,Hkv,D), bf16, no positions"}
+    traffic = measured_traffic(wl.name)
+    for name, mult in (("rope_norm_fwd_bf16", 2), ("rope_norm_bwd_bf16", 3)):
+        n, tot = k[name]
+        per_step_ms = tot / steps  # both tensors
+        achieved = mult * nbytes / (per_step_ms * 1e-3) / 1e9
+        key = "fwd" if "fwd" in name else "bwd"
+        out[key] = {"ms_per_step": round(per_step_ms, 4), "launches": n,
+                    "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                                 # rocprof's bytes per launch (averaged over the Q and K launches) x 2
+                                 "traffic": (2 * traffic[name.replace("_bf16", "")]
+                                             if name.replace("_bf16", "") in traffic else None)}}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +231,8 @@ def main() -> int:
             rec["hbm_bytes"] = traffic[key]
             rec["hbm_gbs"] = round(traffic[key] / (rec["avg_ms"] * 1e-3) / 1e9, 1)
 
+    prologue = measure_prologue(wl, dev, args.steps) if fast else None
+
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -210,6 +261,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": per_kernel,
+        "prologue": prologue,
     }
     print(json.dumps(out), flush=True)
     return 0

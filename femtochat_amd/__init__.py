@@ -2,7 +2,9 @@
 
 The compute path is libfemtochat_attn.so (hand-written gfx950 HIP kernels
 behind a C ABI, include/femtochat_attn.h); ``femtochat_amd.kernels`` is the
-host-side mirror of the reference's ``Kernels`` attention API.
+host-side mirror of the reference's ``Kernels`` attention API, and
+``femtochat_amd.prologue`` the rotary embedding + RMS norm that
+``CausalSelfAttention`` applies to Q and K before it.
 """
 from .kernels import (  # noqa: F401
     AttentionFunction,
@@ -19,6 +21,13 @@ from .kernels import (  # noqa: F401
     delta_attention_,
     instruction,
     window_sizes,
+)
+from .prologue import (  # noqa: F401
+    AttentionPrologueFunction,
+    attention_prologue,
+    attention_prologue_,
+    delta_attention_prologue_,
+    rotary_embeddings,
 )
 
 __version__ = "0.1.0"

@@ -54,6 +54,18 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class RopeNormDesc(ctypes.Structure):
+    _fields_ = [
+        ("D", ctypes.c_int32),
+        ("NH", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("B", ctypes.c_int32),
+        ("table_len", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
 class Caps(ctypes.Structure):
     _fields_ = [
         ("name", ctypes.c_char * 64),
@@ -102,6 +114,8 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(AttnDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
     ),
+    "fc_rope_norm_fwd": (ctypes.c_int, [ctypes.POINTER(RopeNormDesc), _P, _P, _P, _P, _P, _P]),
+    "fc_rope_norm_bwd": (ctypes.c_int, [ctypes.POINTER(RopeNormDesc), _P, _P, _P, _P, _P, _P, _P]),
     "fc_capabilities": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(Caps)]),
     "fc_profile_enable": (ctypes.c_int, [ctypes.c_int32]),
     "fc_profile_collect": (

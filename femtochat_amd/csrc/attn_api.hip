@@ -288,6 +288,71 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, c
   return ok();
 }
 
+// ---- attention prologue (rope_norm.hip) -----------------------------------
+static fc_status rope_norm_args(const fc_rope_norm_desc* d, const void* X, const float* sin_table,
+                                const float* cos_table, const char* who, fc::RopeNormArgs* a) {
+  if (d == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "%s: descriptor is null", who);
+  if (d->D <= 0 || d->NH <= 0 || d->T <= 0 || d->B <= 0 || d->table_len <= 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: sizes must be positive (D=%d NH=%d T=%d B=%d table_len=%d)", who, d->D,
+                d->NH, d->T, d->B, d->table_len);
+  if (d->D % 16 != 0 || d->D > 128)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: head_dim %d must be a multiple of 16 and at most 128", who, d->D);
+  if (d->D != 16 && d->D != 32 && d->D != 64 && d->D != 128)
+    return fail(FC_ERR_UNSUPPORTED, "%s: head_dim %d is not compiled in (supported: 16, 32, 64, 128)", who, d->D);
+  if (!valid_dtype(d->dtype)) return fail(FC_ERR_INVALID_ARGUMENT, "%s: dtype must be FC_F32 or FC_BF16", who);
+  if ((d->flags & ~FC_FLAG_OVERWRITE) != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x", who, d->flags);
+  const int64_t vectors = (int64_t)d->B * d->T * d->NH;
+  if (vectors * (d->D / 8) >= ((int64_t)1 << 31) * 256 || (int64_t)d->table_len * d->D >= INT32_MAX)
+    return fail(FC_ERR_UNSUPPORTED, "%s: problem too large", who);
+  if (X == nullptr || sin_table == nullptr || cos_table == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: a required pointer is null", who);
+  if ((reinterpret_cast<uintptr_t>(sin_table) | reinterpret_cast<uintptr_t>(cos_table) |
+       reinterpret_cast<uintptr_t>(X)) % 16 != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: X and the tables must be 16-byte aligned", who);
+  *a = fc::RopeNormArgs{};
+  a->X = X;
+  a->sin_t = sin_table;
+  a->cos_t = cos_table;
+  a->vectors = vectors;
+  a->NH = d->NH;
+  a->T = d->T;
+  a->table_len = d->table_len;
+  return FC_OK;
+}
+
+fc_status fc_rope_norm_fwd(const fc_rope_norm_desc* desc, const void* X, const float* sin_table,
+                           const float* cos_table, const int32_t* positions, void* Y, void* stream) {
+  fc::RopeNormArgs a;
+  const fc_status st = rope_norm_args(desc, X, sin_table, cos_table, "fc_rope_norm_fwd", &a);
+  if (st != FC_OK) return st;
+  if (Y == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "fc_rope_norm_fwd: Y is null");
+  if (reinterpret_cast<uintptr_t>(Y) % 16 != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_rope_norm_fwd: Y must be 16-byte aligned");
+  a.Y = Y;
+  a.pos = positions;
+  const hipError_t e = fc::launch_rope_norm(desc->D, desc->dtype == FC_BF16, a, false, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "prologue launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+fc_status fc_rope_norm_bwd(const fc_rope_norm_desc* desc, const void* dY, const void* X, const float* sin_table,
+                           const float* cos_table, const int32_t* positions, void* dX, void* stream) {
+  fc::RopeNormArgs a;
+  const fc_status st = rope_norm_args(desc, X, sin_table, cos_table, "fc_rope_norm_bwd", &a);
+  if (st != FC_OK) return st;
+  if (dY == nullptr || dX == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "fc_rope_norm_bwd: dY or dX is null");
+  if ((reinterpret_cast<uintptr_t>(dY) | reinterpret_cast<uintptr_t>(dX)) % 16 != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_rope_norm_bwd: dY and dX must be 16-byte aligned");
+  a.dY = dY;
+  a.dX = dX;
+  a.pos = positions;
+  a.accumulate = (desc->flags & FC_FLAG_OVERWRITE) == 0 ? 1 : 0;
+  const hipError_t e = fc::launch_rope_norm(desc->D, desc->dtype == FC_BF16, a, true, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "prologue backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 fc_status fc_capabilities(int32_t device, fc_caps* caps) {
   if (caps == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "caps is null");
   hipDeviceProp_t prop;

@@ -79,6 +79,22 @@ struct BwdArgs {
   float scale_log2;  // log2(e)/sqrt(D)
 };
 
+// Attention prologue (rope_norm.hip): rotary embedding then RMS norm x 1.2
+// of one tensor (Q or K) with NH heads; vectors = B*T*NH head vectors.
+struct RopeNormArgs {
+  const void* X;
+  void* Y;          // forward output
+  const void* dY;   // backward input
+  void* dX;         // backward output
+  const float* sin_t;  // (table_len, D/2): column p = position p
+  const float* cos_t;
+  const int32_t* pos;  // (B, T) or null: position = token index
+  int64_t vectors;
+  int NH, T, table_len;
+  int accumulate;   // backward adds into dX
+};
+hipError_t launch_rope_norm(int D, bool bf16_storage, const RopeNormArgs& a, bool backward, hipStream_t s);
+
 // Workspace layout of the backward pass (byte offsets, 256-aligned).
 struct BwdWorkspace {
   size_t delta, lse2, chunk_lb, dO16, total;

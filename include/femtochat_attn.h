@@ -104,6 +104,48 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q,
                       void* dQ, void* dK, void* dV, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* ---- Attention prologue ---------------------------------------------------
+ * Rotary embedding followed by the RMS norm over the head dimension scaled by
+ * 1.2, applied to Q or K as CausalSelfAttention does before calling
+ * attention (reference src/gpt.jl:101-106: apply_rotary_embedding :53-77,
+ * norm :15-20; tables from rotary_embeddings, src/parameters.jl:409-427),
+ * writing the result in the attention kernels' layout.
+ *   X, Y, dY, dX  (D,NH,T,B) : X[((b*T + t)*NH + h)*D + d]   (NH = n_head for
+ *                                                             Q, n_kv_head for K)
+ *   sin, cos      (D/2,L)    : s[p*(D/2) + j]  float32, column p = position p
+ *   positions     (T,B)      : p[b*T + t], or NULL for position t (the
+ *                              reference's rotary_factors, src/gpt.jl:43-49)
+ * With d = D/2, c = cos[pos], s = sin[pos]:
+ *   u[j] = x[j] c[j] + x[j+d] s[j],  u[j+d] = -x[j] s[j] + x[j+d] c[j],
+ *   Y = u / sqrt(sum(u^2)/D + eps) * 1.2,  eps = eps(eltype) (2^-7 bf16, 2^-23 f32),
+ * rounded after every operation in bf16 as Julia's BFloat16 arithmetic is.
+ * A position outside [0, L) yields NaN for that vector (an index error in
+ * the reference).  X and the tables must be 16-byte aligned. */
+typedef struct {
+  int32_t D, NH, T, B;  /* head_dim, heads of this tensor, tokens, batch */
+  int32_t table_len;    /* L: columns of the sin/cos tables */
+  int32_t dtype;        /* FC_F32 or FC_BF16: element type of X, Y, dY, dX */
+  uint32_t flags;       /* FC_FLAG_OVERWRITE: the backward writes dX instead of adding */
+} fc_rope_norm_desc;
+
+/* Forward of the prologue: Y from X.  Replaces the four lines
+   `Q = apply_rotary_embedding(Q, rope_cos, rope_sin); ...; Q = eltype(Q).(norm(Q) .* 1.2f0)`
+   (reference src/gpt.jl:103-106) for one tensor. */
+fc_status fc_rope_norm_fwd(const fc_rope_norm_desc* desc, const void* X,
+                           const float* sin_table, const float* cos_table,
+                           const int32_t* positions, void* Y, void* stream);
+
+/* Backward of the prologue: adds (or, with FC_FLAG_OVERWRITE, writes) dX =
+   (dY/dX)^T dY, recomputing the rotation and the norm from X; the gradient
+   of the exact function in fp32 at the rounded rotation.  Replaces the
+   reverse pass the reference gets from Enzyme through those lines
+   (ext/FemtoChatEnzymeExt.jl differentiates the model around the attention
+   rule). */
+fc_status fc_rope_norm_bwd(const fc_rope_norm_desc* desc, const void* dY,
+                           const void* X, const float* sin_table,
+                           const float* cos_table, const int32_t* positions,
+                           void* dX, void* stream);
+
 /* Last error message of the calling thread ("" if none). */
 const char* fc_last_error(void);
 

@@ -303,7 +303,7 @@ static fc_status rope_norm_args(const fc_rope_norm_desc* d, const void* X, const
   if ((d->flags & ~FC_FLAG_OVERWRITE) != 0)
     return fail(FC_ERR_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x", who, d->flags);
   const int64_t vectors = (int64_t)d->B * d->T * d->NH;
-  if (vectors * (d->D / 8) >= ((int64_t)1 << 31) * 256 || (int64_t)d->table_len * d->D >= INT32_MAX)
+  if (vectors >= ((int64_t)1 << 30) || (int64_t)d->table_len * d->D >= INT32_MAX)
     return fail(FC_ERR_UNSUPPORTED, "%s: problem too large", who);
   if (X == nullptr || sin_table == nullptr || cos_table == nullptr)
     return fail(FC_ERR_INVALID_ARGUMENT, "%s: a required pointer is null", who);
@@ -314,9 +314,11 @@ static fc_status rope_norm_args(const fc_rope_norm_desc* d, const void* X, const
   a->X = X;
   a->sin_t = sin_table;
   a->cos_t = cos_table;
-  a->vectors = vectors;
+  a->vectors = (int)vectors;
   a->NH = d->NH;
   a->T = d->T;
+  a->by_NH = fc::fast_div((uint32_t)d->NH);
+  a->by_T = fc::fast_div((uint32_t)d->T);
   a->table_len = d->table_len;
   return FC_OK;
 }

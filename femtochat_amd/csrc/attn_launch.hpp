@@ -81,6 +81,20 @@ struct BwdArgs {
 
 // Attention prologue (rope_norm.hip): rotary embedding then RMS norm x 1.2
 // of one tensor (Q or K) with NH heads; vectors = B*T*NH head vectors.
+// n / d for 0 <= n < 2^31 by a multiply and a shift: with 2^(l-1) < d <= 2^l
+// and m = floor(2^32 (2^l - d) / d) + 1, n / d = (umulhi(n, m) + n) >> l
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994).
+struct FastDiv {
+  uint32_t m;
+  int l;
+};
+inline FastDiv fast_div(uint32_t d) {
+  int l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  return FastDiv{uint32_t((((uint64_t(1) << l) - d) << 32) / d + 1), l};
+}
+
 struct RopeNormArgs {
   const void* X;
   void* Y;          // forward output
@@ -89,8 +103,9 @@ struct RopeNormArgs {
   const float* sin_t;  // (table_len, D/2): column p = position p
   const float* cos_t;
   const int32_t* pos;  // (B, T) or null: position = token index
-  int64_t vectors;
+  int vectors;       // B*T*NH < 2^30
   int NH, T, table_len;
+  FastDiv by_NH, by_T;
   int accumulate;   // backward adds into dX
 };
 hipError_t launch_rope_norm(int D, bool bf16_storage, const RopeNormArgs& a, bool backward, hipStream_t s);

@@ -153,3 +153,33 @@ def test_c3_full_size_properties(gpu):
             ref = R.forward(Xd[b:b + 1].float().cpu().numpy(), sin.numpy(), cos.numpy(), None, "bf16")
             u = _ulp_bf16(Yd[b:b + 1].float().cpu().numpy(), ref)
             assert np.max(u) <= 2.0 and np.mean(u > 0) < 0.01
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_extreme_magnitudes_take_the_exact_division(gpu, dtype):
+    # Vectors whose rotated elements fall below 2^-100, are zero, or whose sum
+    # of squares overflows (norm = inf) leave the reciprocal-and-correction
+    # quotient for a true division; they must still match the oracle.
+    B, T, NH, D = 1, 6, 4, 64
+    g = torch.Generator().manual_seed(21)
+    X = torch.randn(B, T, NH, D, generator=g)
+    X[0, 0, 0, :8] = 1e-33  # both halves of the first pairs tiny
+    X[0, 0, 0, 32:40] = -1e-33
+    X[0, 1, 1, :] = 0.0
+    X[0, 2, 2, 5] = 1e-40  # subnormal element next to normal ones
+    X[0, 2, 2, 37] = -1e-40
+    X[0, 3, 3, :] = 1e20 if dtype == torch.float32 else 1e30  # the float32 sum of squares overflows
+    X[0, 4, 0, :] *= 1e-30
+    X = X.to(dtype)
+    sin, cos = rotary_embeddings(8, D)
+    Y = attention_prologue(X.to(gpu), (sin.to(gpu), cos.to(gpu))).float().cpu().numpy()
+    mode = "bf16" if dtype == torch.bfloat16 else "f32"
+    with np.errstate(over="ignore"):  # the overflowing sum of squares is the case under test
+        ref = R.forward(X.float().numpy(), sin.numpy(), cos.numpy(), None, mode)
+    assert np.array_equal(np.isnan(Y), np.isnan(ref)) and not np.isnan(ref).any()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(Y, ref, rtol=4e-7, atol=1e-44)
+    else:
+        u = _ulp_bf16(Y, ref)
+        assert np.max(u) <= 2.0
+    assert np.all(Y[0, 1, 1] == 0) and np.all(Y[0, 3, 3] == 0)

@@ -145,6 +145,62 @@ def measure_prologue(wl, dev, steps: int) -> dict:
     return out
 
 
+def measure_loss(dev, steps: int) -> dict:
+    """Loss-side kernels at the training step's shape (scripts/train.jl
+    defaults: vocabulary 2^15, 4 x 2048 tokens, 512-wide embeddings; fp32
+    logits and weights): cross-entropy forward (losses, log-sum-exp, mean),
+    its gradient accumulating into the logits' gradient, the embedding gather
+    and its scatter-add gradient.  HBM-bound: algorithmic bytes per unit time
+    against 8 TB/s.  Not part of the headline value."""
+    import torch
+
+    import femtochat_amd._lib as L
+    from femtochat_amd import cross_entropy_, cross_entropy_gradient_, embedding_, embedding_gradient_
+
+    V, N, D = 32768, 4 * 2048, 512
+    g = torch.Generator(device=dev).manual_seed(0)
+    logits = torch.randn(N, V, device=dev, generator=g) * 4
+    targets = torch.randint(0, V, (N,), device=dev, generator=g, dtype=torch.int32)
+    dlogits = torch.zeros_like(logits)
+    losses, lse = torch.empty(N, device=dev), torch.empty(N, device=dev)
+    reduced, count = torch.empty(1, device=dev), torch.empty(1, device=dev)
+    dy = torch.ones(1, device=dev)
+    W = torch.randn(V, D, device=dev, generator=g)
+    dW = torch.zeros_like(W)
+    tokens = torch.randint(0, V, (N,), device=dev, generator=g, dtype=torch.int32)
+    y = torch.empty(N, D, device=dev)
+    dY = torch.randn(N, D, device=dev, generator=g)
+
+    def once():
+        cross_entropy_(losses, logits, targets, -1, "mean", lse=lse, reduced=reduced, count=count)
+        cross_entropy_gradient_(dlogits, logits, targets, dy, -1, "mean", lse=lse, count=count)
+        embedding_(y, W, tokens)
+        embedding_gradient_(dW, dY, tokens)
+
+    for _ in range(3):
+        once()
+    torch.cuda.synchronize()
+    L.profile_collect()
+    L.profile_enable(True)
+    for _ in range(steps):
+        once()
+    torch.cuda.synchronize()
+    L.profile_enable(False)
+    k = L.profile_collect()
+    lg, em = N * V * 4, N * D * 4
+    out = {"workload": f"train.jl step: V={V}, N={N} tokens (B=4, T=2048), D={D}, fp32; uniform random targets/tokens"}
+    # bytes per launch: logits read; logits read + gradient read and written;
+    # weight rows read + output written; dy read + weight rows read and written
+    for name, nbytes in (("xent_fwd", lg), ("xent_bwd", 3 * lg), ("embed_fwd", 2 * em), ("embed_bwd", 3 * em)):
+        n, tot = k[name]
+        ms = tot / steps
+        achieved = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "launches": n, "bytes": nbytes,
+                     "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                                  "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -232,6 +288,7 @@ def main() -> int:
             rec["hbm_gbs"] = round(traffic[key] / (rec["avg_ms"] * 1e-3) / 1e9, 1)
 
     prologue = measure_prologue(wl, dev, args.steps) if fast else None
+    loss_side = measure_loss(dev, args.steps) if fast else None
 
     cpu = None
     if not args.no_cpu:
@@ -262,6 +319,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "kernels": per_kernel,
         "prologue": prologue,
+        "loss": loss_side,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -4,7 +4,9 @@ The compute path is libfemtochat_attn.so (hand-written gfx950 HIP kernels
 behind a C ABI, include/femtochat_attn.h); ``femtochat_amd.kernels`` is the
 host-side mirror of the reference's ``Kernels`` attention API, and
 ``femtochat_amd.prologue`` the rotary embedding + RMS norm that
-``CausalSelfAttention`` applies to Q and K before it.
+``CausalSelfAttention`` applies to Q and K before it, and
+``femtochat_amd.loss`` the cross-entropy and token-embedding kernels either
+side of the model (include/femtochat_loss.h).
 """
 from .kernels import (  # noqa: F401
     AttentionFunction,
@@ -28,6 +30,17 @@ from .prologue import (  # noqa: F401
     attention_prologue_,
     delta_attention_prologue_,
     rotary_embeddings,
+)
+from .loss import (  # noqa: F401
+    CrossEntropyFunction,
+    EmbeddingFunction,
+    cross_entropy,
+    cross_entropy_,
+    cross_entropy_gradient_,
+    embedding,
+    embedding_,
+    embedding_gradient_,
+    valid_target_count,
 )
 
 __version__ = "0.1.0"

@@ -1,4 +1,5 @@
-"""ctypes binding of libfemtochat_attn.so (the C ABI in include/femtochat_attn.h).
+"""ctypes binding of libfemtochat_attn.so (the C ABI in include/femtochat_attn.h
+and include/femtochat_loss.h).
 
 The shared library is built in-tree by ``femtochat_amd.build`` (hipcc,
 gfx950).  Loading fails loudly when it is missing: there is no CPU fallback
@@ -26,6 +27,11 @@ FC_MODE_FAST = 1
 FC_FLAG_OVERWRITE = 1
 FC_PASS_FORWARD = 0
 FC_PASS_BACKWARD = 1
+FC_REDUCE_NONE = 0
+FC_REDUCE_SUM = 1
+FC_REDUCE_MEAN = 2
+FC_INDEX_I32 = 0
+FC_INDEX_I64 = 1
 
 STATUS_NAMES = {
     FC_OK: "FC_OK",
@@ -62,6 +68,30 @@ class RopeNormDesc(ctypes.Structure):
         ("B", ctypes.c_int32),
         ("table_len", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
+class XentDesc(ctypes.Structure):
+    _fields_ = [
+        ("V", ctypes.c_int32),
+        ("index_base", ctypes.c_int32),
+        ("N", ctypes.c_int64),
+        ("ignore_index", ctypes.c_int64),
+        ("index_type", ctypes.c_int32),
+        ("reduction", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
+class EmbedDesc(ctypes.Structure):
+    _fields_ = [
+        ("D", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("N", ctypes.c_int64),
+        ("index_base", ctypes.c_int32),
+        ("index_type", ctypes.c_int32),
+        ("y_dtype", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
     ]
 
@@ -116,6 +146,11 @@ _SIGNATURES = {
     ),
     "fc_rope_norm_fwd": (ctypes.c_int, [ctypes.POINTER(RopeNormDesc), _P, _P, _P, _P, _P, _P]),
     "fc_rope_norm_bwd": (ctypes.c_int, [ctypes.POINTER(RopeNormDesc), _P, _P, _P, _P, _P, _P, _P]),
+    "fc_cross_entropy_fwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P]),
+    "fc_cross_entropy_count": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P]),
+    "fc_cross_entropy_bwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P]),
+    "fc_embedding_fwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
+    "fc_embedding_bwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
     "fc_capabilities": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(Caps)]),
     "fc_profile_enable": (ctypes.c_int, [ctypes.c_int32]),
     "fc_profile_collect": (

@@ -6,6 +6,7 @@
 // foreign boundary (ext/reactant/cuda_call.jl:45-48): every failure becomes an
 // fc_status plus a thread-local message.
 #include "../../include/femtochat_attn.h"
+#include "../../include/femtochat_loss.h"
 #include "attn_launch.hpp"
 
 #include <hip/hip_runtime.h>
@@ -352,6 +353,136 @@ fc_status fc_rope_norm_bwd(const fc_rope_norm_desc* desc, const void* dY, const 
   a.accumulate = (desc->flags & FC_FLAG_OVERWRITE) == 0 ? 1 : 0;
   const hipError_t e = fc::launch_rope_norm(desc->D, desc->dtype == FC_BF16, a, true, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(FC_ERR_HIP, "prologue backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+// ---- loss side (loss.hip) ------------------------------------------------------
+static bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; }
+
+static fc_status xent_args(const fc_xent_desc* d, const void* targets, const char* who, fc::XentArgs* a) {
+  if (d == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "%s: descriptor is null", who);
+  if (d->V <= 0 || d->N <= 0) return fail(FC_ERR_INVALID_ARGUMENT, "%s: V and N must be positive (V=%d N=%lld)", who, d->V, (long long)d->N);
+  if (d->N > INT32_MAX) return fail(FC_ERR_UNSUPPORTED, "%s: at most 2^31-1 tokens per call", who);
+  if (d->index_base != 0 && d->index_base != 1) return fail(FC_ERR_INVALID_ARGUMENT, "%s: index_base must be 0 or 1", who);
+  if (d->index_type != FC_INDEX_I32 && d->index_type != FC_INDEX_I64)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: index_type must be FC_INDEX_I32 or FC_INDEX_I64", who);
+  if (d->reduction < FC_REDUCE_NONE || d->reduction > FC_REDUCE_MEAN)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: unknown reduction %d", who, d->reduction);
+  if ((d->flags & ~FC_FLAG_OVERWRITE) != 0) return fail(FC_ERR_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x", who, d->flags);
+  if (targets == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "%s: targets is null", who);
+  if ((reinterpret_cast<uintptr_t>(targets) & (d->index_type == FC_INDEX_I64 ? 7 : 3)) != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: targets are not aligned to their element size", who);
+  *a = fc::XentArgs{};
+  a->targets = targets;
+  a->N = d->N;
+  a->V = d->V;
+  a->ignore_index = d->ignore_index;
+  a->index_base = d->index_base;
+  a->index_type = d->index_type;
+  a->reduction = d->reduction;
+  a->overwrite = (d->flags & FC_FLAG_OVERWRITE) != 0;
+  return FC_OK;
+}
+
+fc_status fc_cross_entropy_fwd(const fc_xent_desc* desc, const float* logits, const void* targets, float* losses,
+                               float* lse, float* reduced, float* count, void* stream) {
+  fc::XentArgs a;
+  const fc_status st = xent_args(desc, targets, "fc_cross_entropy_fwd", &a);
+  if (st != FC_OK) return st;
+  if (logits == nullptr || losses == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_fwd: logits and losses are required");
+  if (!aligned4(logits) || !aligned4(losses) || !aligned4(lse) || !aligned4(reduced) || !aligned4(count))
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_fwd: float buffers must be 4-byte aligned");
+  a.logits = logits;
+  a.losses = losses;
+  a.lse = lse;
+  a.reduced = reduced;
+  a.count = count;
+  const hipError_t e = fc::launch_xent_fwd(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "cross-entropy launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+fc_status fc_cross_entropy_count(const fc_xent_desc* desc, const void* targets, float* count, void* stream) {
+  fc::XentArgs a;
+  const fc_status st = xent_args(desc, targets, "fc_cross_entropy_count", &a);
+  if (st != FC_OK) return st;
+  if (count == nullptr || !aligned4(count)) return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_count: count is null or misaligned");
+  a.count = count;
+  const hipError_t e = fc::launch_xent_count(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "count launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+fc_status fc_cross_entropy_bwd(const fc_xent_desc* desc, float* dlogits, const float* logits, const void* targets,
+                               const float* dy, const float* count, const float* lse, void* stream) {
+  fc::XentArgs a;
+  const fc_status st = xent_args(desc, targets, "fc_cross_entropy_bwd", &a);
+  if (st != FC_OK) return st;
+  if (dlogits == nullptr || logits == nullptr || dy == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_bwd: dlogits, logits and dy are required");
+  if (desc->reduction == FC_REDUCE_MEAN && count == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_bwd: the mean gradient needs the valid-target count");
+  if (!aligned4(dlogits) || !aligned4(logits) || !aligned4(dy) || !aligned4(count) || !aligned4(lse))
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_bwd: float buffers must be 4-byte aligned");
+  a.dlogits = dlogits;
+  a.logits = logits;
+  a.dy = dy;
+  a.count = const_cast<float*>(count);
+  a.lse_in = lse;
+  const hipError_t e = fc::launch_xent_bwd(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "cross-entropy gradient launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+static fc_status embed_args(const fc_embed_desc* d, const void* tokens, const char* who, fc::EmbedArgs* a) {
+  if (d == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "%s: descriptor is null", who);
+  if (d->D <= 0 || d->vocab <= 0 || d->N <= 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: D, vocab and N must be positive (D=%d vocab=%d N=%lld)", who, d->D, d->vocab,
+                (long long)d->N);
+  if ((d->N + 3) / 4 > INT32_MAX) return fail(FC_ERR_UNSUPPORTED, "%s: too many tokens per call", who);
+  if (d->index_base != 0 && d->index_base != 1) return fail(FC_ERR_INVALID_ARGUMENT, "%s: index_base must be 0 or 1", who);
+  if (d->index_type != FC_INDEX_I32 && d->index_type != FC_INDEX_I64)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: index_type must be FC_INDEX_I32 or FC_INDEX_I64", who);
+  if (!valid_dtype(d->y_dtype)) return fail(FC_ERR_INVALID_ARGUMENT, "%s: y_dtype must be FC_F32 or FC_BF16", who);
+  if (d->flags != 0) return fail(FC_ERR_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x", who, d->flags);
+  if (tokens == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "%s: tokens is null", who);
+  if ((reinterpret_cast<uintptr_t>(tokens) & (d->index_type == FC_INDEX_I64 ? 7 : 3)) != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: tokens are not aligned to their element size", who);
+  *a = fc::EmbedArgs{};
+  a->tokens = tokens;
+  a->N = d->N;
+  a->D = d->D;
+  a->vocab = d->vocab;
+  a->index_base = d->index_base;
+  a->index_type = d->index_type;
+  return FC_OK;
+}
+
+fc_status fc_embedding_fwd(const fc_embed_desc* desc, const float* weights, const void* tokens, void* y, void* stream) {
+  fc::EmbedArgs a;
+  const fc_status st = embed_args(desc, tokens, "fc_embedding_fwd", &a);
+  if (st != FC_OK) return st;
+  if (weights == nullptr || y == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_fwd: weights and y are required");
+  if (!aligned4(weights) || (reinterpret_cast<uintptr_t>(y) & (desc->y_dtype == FC_BF16 ? 1 : 3)) != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_fwd: buffers are not aligned to their element size");
+  a.weights = weights;
+  a.y = y;
+  const hipError_t e = fc::launch_embed(a, false, desc->y_dtype == FC_BF16, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "embedding launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+fc_status fc_embedding_bwd(const fc_embed_desc* desc, float* dweights, const void* dy, const void* tokens, void* stream) {
+  fc::EmbedArgs a;
+  const fc_status st = embed_args(desc, tokens, "fc_embedding_bwd", &a);
+  if (st != FC_OK) return st;
+  if (dweights == nullptr || dy == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_bwd: dweights and dy are required");
+  if (!aligned4(dweights) || (reinterpret_cast<uintptr_t>(dy) & (desc->y_dtype == FC_BF16 ? 1 : 3)) != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_bwd: buffers are not aligned to their element size");
+  a.dweights = dweights;
+  a.dy = dy;
+  const hipError_t e = fc::launch_embed(a, true, desc->y_dtype == FC_BF16, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "embedding gradient launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

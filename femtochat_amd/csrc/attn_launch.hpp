@@ -110,6 +110,41 @@ struct RopeNormArgs {
 };
 hipError_t launch_rope_norm(int D, bool bf16_storage, const RopeNormArgs& a, bool backward, hipStream_t s);
 
+// Cross-entropy over vocabulary columns (loss.hip).
+struct XentArgs {
+  const float* logits;   // (V, N) column-major: token t's column at t*V
+  const void* targets;   // N indices (int32 or int64)
+  float* losses;         // N (forward)
+  float* lse;            // N or null (forward: log-sum-exp per token)
+  float* reduced;        // null or [1]: sum or mean of the losses
+  float* count;          // null or [1]: number of valid targets (forward, count); read by the mean gradient
+  float* dlogits;        // (V, N) (backward)
+  const float* dy;       // 1 value (sum, mean) or N (none) (backward)
+  const float* lse_in;   // N or null (backward: recompute)
+  int64_t N;
+  int V;
+  int64_t ignore_index;
+  int index_base, index_type;  // index_type 0: int32, 1: int64
+  int reduction;               // 0 none, 1 sum, 2 mean
+  int overwrite;               // backward writes instead of adding
+};
+hipError_t launch_xent_fwd(const XentArgs& a, hipStream_t s);
+hipError_t launch_xent_count(const XentArgs& a, hipStream_t s);
+hipError_t launch_xent_bwd(const XentArgs& a, hipStream_t s);
+
+// Embedding gather and scatter-add (loss.hip).
+struct EmbedArgs {
+  const float* weights;  // (D, vocab) column-major
+  float* dweights;
+  const void* tokens;    // N indices
+  void* y;               // (D, N), float32 or bf16
+  const void* dy;        // (D, N), float32 or bf16
+  int64_t N;
+  int D, vocab;
+  int index_base, index_type;
+};
+hipError_t launch_embed(const EmbedArgs& a, bool backward, bool bf16_y, hipStream_t s);
+
 // Workspace layout of the backward pass (byte offsets, 256-aligned).
 struct BwdWorkspace {
   size_t delta, lse2, chunk_lb, dO16, total;

@@ -15,27 +15,33 @@ import femtochat_amd._lib as L
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "femtochat_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
-def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(fc_[a-z_0-9]+)\s*\(", text)))
+def declared_functions(header=None):
+    names = set()
+    for h in ([header] if header else HEADERS):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(fc_[a-z_0-9]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_exports_every_declared_symbol():
     lib = L.lib()
     names = declared_functions()
-    assert len(names) >= 9, names
+    assert len(names) >= 15, names
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in {HEADER.name} but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
+        assert n in L._SIGNATURES, f"{n} has no ctypes signature"
 
 
 def test_header_compiles_as_c_and_cpp():
-    for lang, cc in (("c", "gcc"), ("c++", "g++")):
-        r = subprocess.run([cc, "-x", lang, "-fsyntax-only", "-Wall", "-Werror", str(HEADER)], capture_output=True,
-                           text=True)
-        assert r.returncode == 0, r.stderr
+    assert len(HEADERS) >= 2
+    for h in HEADERS:
+        for lang, cc in (("c", "gcc"), ("c++", "g++")):
+            r = subprocess.run([cc, "-x", lang, "-fsyntax-only", "-Wall", "-Werror", str(h)], capture_output=True,
+                               text=True)
+            assert r.returncode == 0, (h.name, r.stderr)
 
 
 def test_abi_version_and_head_dims():
@@ -136,3 +142,52 @@ def test_last_error_is_cleared_on_success():
 def test_profile_collect_empty():
     L.profile_enable(False)
     assert L.profile_collect() == {}
+
+
+def _xent(**kw):
+    d = L.XentDesc()
+    d.V, d.N, d.index_base, d.ignore_index = kw.get("V", 100), kw.get("N", 8), kw.get("index_base", 0), -1
+    d.index_type, d.reduction, d.flags = kw.get("index_type", 0), kw.get("reduction", 2), kw.get("flags", 0)
+    return d
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(V=0), "positive"), (dict(N=0), "positive"), (dict(index_base=2), "index_base"),
+    (dict(index_type=3), "index_type"), (dict(reduction=5), "reduction"), (dict(flags=4), "flag"),
+])
+def test_cross_entropy_rejects_bad_descriptors(kw, msg):
+    lib = L.lib()
+    fake = ctypes.c_void_p(0x1000)
+    st = lib.fc_cross_entropy_fwd(ctypes.byref(_xent(**kw)), fake, fake, fake, None, None, None, None)
+    assert st == L.FC_ERR_INVALID_ARGUMENT
+    assert msg in lib.fc_last_error().decode()
+
+
+def test_cross_entropy_pointer_checks():
+    lib = L.lib()
+    fake = ctypes.c_void_p(0x1000)
+    d = _xent()
+    assert lib.fc_cross_entropy_fwd(ctypes.byref(d), fake, None, fake, None, None, None, None) == L.FC_ERR_INVALID_ARGUMENT
+    assert lib.fc_cross_entropy_fwd(ctypes.byref(d), None, fake, fake, None, None, None, None) == L.FC_ERR_INVALID_ARGUMENT
+    # the mean gradient needs the valid-target count
+    assert lib.fc_cross_entropy_bwd(ctypes.byref(d), fake, fake, fake, fake, None, None, None) == L.FC_ERR_INVALID_ARGUMENT
+    assert "count" in lib.fc_last_error().decode()
+    # misaligned int64 targets
+    d64 = _xent(index_type=1)
+    assert lib.fc_cross_entropy_fwd(ctypes.byref(d64), fake, ctypes.c_void_p(0x1004), fake, None, None, None,
+                                    None) == L.FC_ERR_INVALID_ARGUMENT
+    assert lib.fc_cross_entropy_count(ctypes.byref(d), fake, None, None) == L.FC_ERR_INVALID_ARGUMENT
+
+
+def test_embedding_rejects_bad_descriptors():
+    lib = L.lib()
+    fake = ctypes.c_void_p(0x1000)
+    d = L.EmbedDesc()
+    d.D, d.vocab, d.N, d.index_base, d.index_type, d.y_dtype, d.flags = 64, 100, 8, 0, 0, 0, 0
+    for field, bad in (("D", 0), ("vocab", -1), ("N", 0), ("index_base", 3), ("y_dtype", 7), ("flags", 1)):
+        e = L.EmbedDesc.from_buffer_copy(d)
+        setattr(e, field, bad)
+        assert lib.fc_embedding_fwd(ctypes.byref(e), fake, fake, fake, None) == L.FC_ERR_INVALID_ARGUMENT, field
+        assert lib.fc_embedding_bwd(ctypes.byref(e), fake, fake, fake, None) == L.FC_ERR_INVALID_ARGUMENT, field
+    assert lib.fc_embedding_fwd(ctypes.byref(d), None, fake, fake, None) == L.FC_ERR_INVALID_ARGUMENT
+    assert lib.fc_embedding_bwd(ctypes.byref(d), fake, None, fake, None) == L.FC_ERR_INVALID_ARGUMENT

@@ -1,5 +1,5 @@
 """ctypes binding of libfemtochat_attn.so (the C ABI in include/femtochat_attn.h
-and include/femtochat_loss.h).
+include/femtochat_loss.h and include/femtochat_xla.h).
 
 The shared library is built in-tree by ``femtochat_amd.build`` (hipcc,
 gfx950).  Loading fails loudly when it is missing: there is no CPU fallback
@@ -117,6 +117,10 @@ class KernelTime(ctypes.Structure):
     ]
 
 
+# The callback type of an XLA FFI call site: bool callback(void* stream, void** buffers).
+XLA_CALLBACK = ctypes.CFUNCTYPE(ctypes.c_bool, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p))
+
+
 class AttentionError(RuntimeError):
     """A non-zero fc_status from the library, with its message."""
 
@@ -151,6 +155,12 @@ _SIGNATURES = {
     "fc_cross_entropy_bwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P]),
     "fc_embedding_fwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
     "fc_embedding_bwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
+    "fc_xla_bind_attention_fwd": (ctypes.c_void_p, [ctypes.POINTER(AttnDesc), ctypes.c_int32]),
+    "fc_xla_bind_attention_bwd": (ctypes.c_void_p, [ctypes.POINTER(AttnDesc), ctypes.c_int32,
+                                                    ctypes.POINTER(ctypes.c_size_t)]),
+    "fc_xla_bind_embedding_fwd": (ctypes.c_void_p, [ctypes.POINTER(EmbedDesc)]),
+    "fc_xla_bind_embedding_bwd": (ctypes.c_void_p, [ctypes.POINTER(EmbedDesc)]),
+    "fc_xla_last_error": (ctypes.c_char_p, []),
     "fc_capabilities": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(Caps)]),
     "fc_profile_enable": (ctypes.c_int, [ctypes.c_int32]),
     "fc_profile_collect": (

@@ -201,6 +201,78 @@ def measure_loss(dev, steps: int) -> dict:
     return out
 
 
+def measure_optim(dev, steps: int) -> dict:
+    """Optimizer kernels at the training model's sizes (scripts/train.jl
+    defaults: n_embed 512, 8 layers, vocabulary 2^15): one AdamW step over
+    2^26 fp32 parameters (the embedding, value-embedding and head matrices'
+    scale), Muon's final write over the block matrices, and Polar Express
+    (5 steps, fp32) over their stacks: 32 of 512x512, 8 of 512x2048 and 8 of
+    2048x512.  AdamW and the write are HBM-bound (bytes per unit time against
+    8 TB/s); Polar Express is GEMMs (rocBLAS): FLOP per unit time against the
+    fp32 MFMA peak.  Not part of the headline value."""
+    import torch
+
+    from femtochat_amd import AdamW, muon_update_, polar_express_
+    from femtochat_amd.optim import polar_workspace_bytes
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    n = 1 << 26
+    theta = torch.randn(n, device=dev, generator=g)
+    grad = torch.randn(n, device=dev, generator=g)
+    opt = AdamW(theta, alpha=0.004, beta1=0.8, beta2=0.96, eps=1e-10, lam=0.01)
+    shapes = [(512, 512, 32), (512, 2048, 8), (2048, 512, 8)]  # Julia (m, n, k)
+    stacks = [torch.randn(k, nn, mm, device=dev, generator=g) for mm, nn, k in shapes]
+    work = [torch.empty(polar_workspace_bytes(G), dtype=torch.uint8, device=dev) for G in stacks]
+    flat_n = sum(G.numel() for G in stacks)
+    Theta = torch.randn(flat_n, device=dev, generator=g)
+    offs, pos = [], 0
+    for G in stacks:
+        w = G[0].numel()
+        offs.append(torch.arange(G.shape[0], device=dev, dtype=torch.int64) * w + pos)
+        pos += G.numel()
+    eta, lam = torch.tensor([0.02], device=dev), torch.tensor([0.01], device=dev)
+
+    def timed(fn, reps):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    out = {"workload": "train.jl model: AdamW over 2^26 fp32 parameters; Muon stacks 32x(512x512), "
+                       "8x(512x2048), 8x(2048x512), fp32, 5 Polar Express steps"}
+    ms = timed(lambda: opt(theta, grad), steps)
+    nbytes = 28 * n  # theta, grad, m, v read; theta, m, v written
+    out["adamw"] = {"ms": round(ms, 4), "bytes": nbytes, "roofline": _hbm_roofline(nbytes, ms)}
+    for G, o in zip(stacks, offs):  # offsets checked once, outside the timed region
+        muon_update_(Theta, G.reshape(G.shape[0], -1), eta, lam, o)
+    ms = timed(lambda: [muon_update_(Theta, G.reshape(G.shape[0], -1), eta, lam, o, validate=False)
+                        for G, o in zip(stacks, offs)], steps)
+    nbytes = 12 * flat_n  # Theta read and written, X read
+    out["muon_update"] = {"ms": round(ms, 4), "bytes": nbytes, "roofline": _hbm_roofline(nbytes, ms)}
+    flops = 0
+    for mm, nn, k in shapes:
+        lo, hi = min(mm, nn), max(mm, nn)
+        flops += 5 * k * (4 * lo * lo * hi + 2 * lo ** 3)
+    ms = timed(lambda: [polar_express_(G, 5, w) for G, w in zip(stacks, work)], max(2, steps // 4))
+    achieved = flops / (ms * 1e-3) / 1e12
+    out["polar_express"] = {"ms": round(ms, 4), "flop": flops,
+                            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
+                                         "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4)}}
+    return out
+
+
+def _hbm_roofline(nbytes: int, ms: float) -> dict:
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -289,6 +361,7 @@ def main() -> int:
 
     prologue = measure_prologue(wl, dev, args.steps) if fast else None
     loss_side = measure_loss(dev, args.steps) if fast else None
+    optim_side = measure_optim(dev, args.steps) if fast else None
 
     cpu = None
     if not args.no_cpu:
@@ -320,6 +393,7 @@ def main() -> int:
         "kernels": per_kernel,
         "prologue": prologue,
         "loss": loss_side,
+        "optim": optim_side,
     }
     print(json.dumps(out), flush=True)
     return 0

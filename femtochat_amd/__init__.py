@@ -6,7 +6,8 @@ host-side mirror of the reference's ``Kernels`` attention API, and
 ``femtochat_amd.prologue`` the rotary embedding + RMS norm that
 ``CausalSelfAttention`` applies to Q and K before it, and
 ``femtochat_amd.loss`` the cross-entropy and token-embedding kernels either
-side of the model (include/femtochat_loss.h).
+side of the model (include/femtochat_loss.h), ``femtochat_amd.optim`` the
+optimizer kernels (include/femtochat_optim.h).
 """
 from .kernels import (  # noqa: F401
     AttentionFunction,
@@ -41,6 +42,16 @@ from .loss import (  # noqa: F401
     embedding_,
     embedding_gradient_,
     valid_target_count,
+)
+from .optim import (  # noqa: F401
+    AdamW,
+    adam_update_,
+    adamw_step_,
+    gather_,
+    muon_update_,
+    polar_express,
+    polar_express_,
+    scatter_,
 )
 
 __version__ = "0.1.0"

@@ -1,5 +1,5 @@
 """ctypes binding of libfemtochat_attn.so (the C ABI in include/femtochat_attn.h
-include/femtochat_loss.h and include/femtochat_xla.h).
+include/femtochat_loss.h, include/femtochat_optim.h and include/femtochat_xla.h).
 
 The shared library is built in-tree by ``femtochat_amd.build`` (hipcc,
 gfx950).  Loading fails loudly when it is missing: there is no CPU fallback
@@ -96,6 +96,29 @@ class EmbedDesc(ctypes.Structure):
     ]
 
 
+class AdamWDesc(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_int64),
+        ("t", ctypes.c_int32),
+        ("alpha", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("lam", ctypes.c_float),
+        ("grad_scale", ctypes.c_float),
+    ]
+
+
+class PolarDesc(ctypes.Structure):
+    _fields_ = [
+        ("m", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("count", ctypes.c_int32),
+        ("steps", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 class Caps(ctypes.Structure):
     _fields_ = [
         ("name", ctypes.c_char * 64),
@@ -161,6 +184,14 @@ _SIGNATURES = {
     "fc_xla_bind_embedding_fwd": (ctypes.c_void_p, [ctypes.POINTER(EmbedDesc)]),
     "fc_xla_bind_embedding_bwd": (ctypes.c_void_p, [ctypes.POINTER(EmbedDesc)]),
     "fc_xla_last_error": (ctypes.c_char_p, []),
+    "fc_adamw_step": (ctypes.c_int, [ctypes.POINTER(AdamWDesc), _P, _P, _P, _P, _P]),
+    "fc_adam_update": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
+                                      _P, _P, _P, _P, _P, _P, _P]),
+    "fc_muon_update": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int32, _P, _P, _P, _P, _P, _P]),
+    "fc_param_gather": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int32, _P, _P, _P, _P]),
+    "fc_param_scatter": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int32, _P, _P, _P, _P]),
+    "fc_polar_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(PolarDesc), ctypes.POINTER(ctypes.c_size_t)]),
+    "fc_polar_express": (ctypes.c_int, [ctypes.POINTER(PolarDesc), _P, _P, ctypes.c_size_t, _P]),
     "fc_capabilities": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(Caps)]),
     "fc_profile_enable": (ctypes.c_int, [ctypes.c_int32]),
     "fc_profile_collect": (

@@ -15,7 +15,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
-SOURCES = ["attn_api.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_fwd_fast.hip", "attn_bwd_fast.hip", "rope_norm.hip", "loss.hip", "xla_bridge.hip"]
+SOURCES = ["attn_api.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_fwd_fast.hip", "attn_bwd_fast.hip", "rope_norm.hip", "loss.hip", "xla_bridge.hip", "optim.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -62,7 +62,10 @@ def build(verbose: bool = False) -> Path:
                 print(err)
     out = PKG / "libfemtochat_attn.so"
     tmp = out.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    rocm_lib = Path(cc).resolve().parent.parent / "lib"
+    # rocBLAS: the batched GEMMs of Polar Express (optim.hip)
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), f"-L{rocm_lib}",
+          f"-Wl,-rpath,{rocm_lib}", "-lrocblas"])
     os.replace(tmp, out)
     return out
 

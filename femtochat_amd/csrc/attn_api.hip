@@ -41,6 +41,19 @@ fc_status ok() {
   return FC_OK;
 }
 
+}  // namespace
+
+namespace fc {
+// Shared with the other translation units of the library (fc_last_error).
+fc_status set_error(fc_status code, const char* message) {
+  g_last_error = message;
+  return code;
+}
+void clear_error() { g_last_error.clear(); }
+}  // namespace fc
+
+namespace {
+
 bool valid_dtype(int32_t d) { return d == FC_F32 || d == FC_BF16; }
 
 // Validates the descriptor and fills the normalised problem.

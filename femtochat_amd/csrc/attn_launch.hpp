@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include "../../include/femtochat_attn.h"
 #include <stddef.h>
 #include <stdint.h>
 
@@ -109,6 +111,10 @@ struct RopeNormArgs {
   int accumulate;   // backward adds into dX
 };
 hipError_t launch_rope_norm(int D, bool bf16_storage, const RopeNormArgs& a, bool backward, hipStream_t s);
+
+// The thread-local error message returned by fc_last_error (attn_api.hip).
+fc_status set_error(fc_status code, const char* message);
+void clear_error();
 
 // Cross-entropy over vocabulary columns (loss.hip).
 struct XentArgs {

@@ -1,0 +1,408 @@
+// Optimizer kernels (gfx950) and their C ABI (include/femtochat_optim.h).
+//
+// Elementwise updates follow the reference's operation order in fp32 without
+// contraction (Julia does not fuse multiply-adds), so they agree bit for bit
+// with a float32 restatement: the AdamW step (src/optim.jl:32-38,82-94), the
+// CUDA final writes (ext/FemtoChatCUDAExt.jl:99-119) and the parameter
+// gather/scatter (src/optim.jl:262-276).  All are HBM-bound: 16-byte
+// accesses where the sizes allow, a scalar tail otherwise.
+//
+// Polar Express (src/optim.jl:115-149) normalises each matrix by its
+// Frobenius norm (one workgroup per matrix), copies it into the iteration
+// buffer (transposed through LDS when m > n, so the Gram matrix is the
+// smaller one), runs three strided-batched rocBLAS GEMMs per step with the
+// elementwise terms folded into their beta, and copies the result back.
+#include "../../include/femtochat_optim.h"
+#include "attn_launch.hpp"
+#include "attn_device.hpp"
+
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <utility>
+
+#pragma clang fp contract(off)
+
+namespace fc {
+namespace {
+
+fc_status failf(fc_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+fc_status failf(fc_status code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  return set_error(code, buf);
+}
+
+fc_status launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return failf(FC_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+  clear_error();
+  return FC_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+unsigned grid_for(int64_t items, int per_block = 256, int64_t cap = 65536) {
+  const int64_t b = (items + per_block - 1) / per_block;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, cap));
+}
+
+// Julia's Float32 ^ Int (t >= 1): x*x*x in Float32 for t = 3, otherwise
+// square-and-multiply in Float64 rounded to Float32.
+float julia_pow(float x, int t) {
+  if (t == 3) return (x * x) * x;
+  double y = 1.0, b = (double)x;
+  bool first = true;
+  for (int p = t; p > 0; p >>= 1) {
+    if (p & 1) {
+      y = first ? b : y * b;
+      first = false;
+    }
+    if (p > 1) b = b * b;
+  }
+  return (float)y;
+}
+
+// ---- AdamW ----------------------------------------------------------------------
+struct AdamScalars {
+  float b1, omb1, b2, omb2, decay, c1, c2, alpha, eps, nscale;
+};
+
+__device__ inline void adamw_one(float& th, float g, float& m, float& v, const AdamScalars& s) {
+  const float gn = g / s.nscale;
+  m = s.b1 * m + s.omb1 * gn;
+  v = s.b2 * v + s.omb2 * (gn * gn);
+  th = th * s.decay;
+  th = th - (s.alpha * (m / s.c1)) / (sqrtf(v / s.c2) + s.eps);
+}
+
+__global__ __launch_bounds__(256) void adamw_kernel(int64_t n, float* th, const float* g, float* m, float* v,
+                                                    AdamScalars s, bool vec) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nv = vec ? n / 4 : 0;
+  for (int64_t c = i0; c < nv; c += stride) {
+    f32x4 T = reinterpret_cast<f32x4*>(th)[c], G = reinterpret_cast<const f32x4*>(g)[c];
+    f32x4 M = reinterpret_cast<f32x4*>(m)[c], Vv = reinterpret_cast<f32x4*>(v)[c];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float t = T[k], mm = M[k], vv = Vv[k];
+      adamw_one(t, G[k], mm, vv, s);
+      T[k] = t;
+      M[k] = mm;
+      Vv[k] = vv;
+    }
+    reinterpret_cast<f32x4*>(th)[c] = T;
+    reinterpret_cast<f32x4*>(m)[c] = M;
+    reinterpret_cast<f32x4*>(v)[c] = Vv;
+  }
+  for (int64_t i = 4 * nv + i0; i < n; i += stride) adamw_one(th[i], g[i], m[i], v[i], s);
+}
+
+__global__ __launch_bounds__(256) void adam_update_kernel(int64_t n, float* Th, const float* m, const float* v,
+                                                          const float* alpha, const float* beta, const float* eta,
+                                                          float lambda, float eps) {
+  const float a = *alpha, b = *beta, decay = 1.0f - *eta * lambda;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+    Th[i] = Th[i] * decay - (a * m[i]) / (sqrtf(v[i] / b) + eps);
+}
+
+// ---- Muon -------------------------------------------------------------------------
+__device__ inline float muon_one(float th, float x, float eta, float lambda) {
+  // eta x + ((eta lambda) th) * (x th >= 0), where Float32 * false is a zero
+  // with the product's sign (Julia's Bool multiplication)
+  float decay = (eta * lambda) * th;
+  if (!(x * th >= 0.0f)) decay = copysignf(0.0f, decay);
+  return th - (eta * x + decay);
+}
+
+__global__ __launch_bounds__(256) void muon_kernel(int64_t width, float* Th, const float* X, const float* eta,
+                                                   const float* lambda, const int64_t* offsets) {
+  const int k = blockIdx.y;
+  const float h = *eta, l = *lambda;
+  float* t = Th + offsets[k];
+  const float* x = X + (int64_t)k * width;
+  const int64_t stride = (int64_t)gridDim.x * 256, i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // 16-byte accesses when this matrix's slices are aligned (uniform per workgroup)
+  const int64_t nv = ((reinterpret_cast<uintptr_t>(t) | reinterpret_cast<uintptr_t>(x)) & 15) == 0 ? width / 4 : 0;
+  for (int64_t c = i0; c < nv; c += stride) {
+    f32x4 T = reinterpret_cast<f32x4*>(t)[c];
+    const f32x4 Xv = reinterpret_cast<const f32x4*>(x)[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) T[e] = muon_one(T[e], Xv[e], h, l);
+    reinterpret_cast<f32x4*>(t)[c] = T;
+  }
+  for (int64_t i = 4 * nv + i0; i < width; i += stride) t[i] = muon_one(t[i], x[i], h, l);
+}
+
+template <bool kGather>
+__global__ __launch_bounds__(256) void param_copy_kernel(int64_t width, float* stack, float* vector,
+                                                         const int64_t* offsets) {
+  const int k = blockIdx.y;
+  float* s = stack + (int64_t)k * width;
+  float* v = vector + offsets[k];
+  const int64_t stride = (int64_t)gridDim.x * 256, i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nv = ((reinterpret_cast<uintptr_t>(s) | reinterpret_cast<uintptr_t>(v)) & 15) == 0 ? width / 4 : 0;
+  for (int64_t c = i0; c < nv; c += stride) {
+    if (kGather) reinterpret_cast<f32x4*>(s)[c] = reinterpret_cast<const f32x4*>(v)[c];
+    else reinterpret_cast<f32x4*>(v)[c] = reinterpret_cast<const f32x4*>(s)[c];
+  }
+  for (int64_t i = 4 * nv + i0; i < width; i += stride) {
+    if (kGather) s[i] = v[i];
+    else v[i] = s[i];
+  }
+}
+
+// ---- Polar Express -------------------------------------------------------------------
+// scale[k] = 1.01 sqrt(sum G_k^2) + 1e-6 (sum in float64).
+__global__ __launch_bounds__(1024) void frobenius_kernel(int64_t size, const float* G, float* scale) {
+  __shared__ double part[16];
+  const float* g = G + (int64_t)blockIdx.x * size;
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < size; i += 1024) s += (double)g[i] * (double)g[i];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < 16; ++w) t += part[w];
+    scale[blockIdx.x] = 1.01f * sqrtf((float)t) + 1e-6f;
+  }
+}
+
+// dst (rows R, cols C, column-major) = src^T / scale (src: C rows, R cols) or
+// src / scale, per matrix (blockIdx.z), through a 32x32 LDS tile.
+template <bool kTranspose>
+__global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const float* src, float* dst,
+                                                          const float* scale) {
+  __shared__ float tile[32][33];
+  const int64_t mat = (int64_t)R * C;
+  const float* s = src + blockIdx.z * mat;
+  float* d = dst + blockIdx.z * mat;
+  const int r0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x / 32;  // 32 x 8
+  if (kTranspose) {
+    // d(r, c) = s(c, r): load s's columns r0.. (contiguous in c), store d's columns c0.. (contiguous in r)
+    for (int j = ty; j < 32; j += 8) {
+      const int r = r0 + j, c = c0 + tx;
+      if (r < R && c < C) tile[j][tx] = s[(int64_t)r * C + c];
+    }
+    __syncthreads();
+    for (int j = ty; j < 32; j += 8) {
+      const int c = c0 + j, r = r0 + tx;
+      if (r < R && c < C) d[(int64_t)c * R + r] = scale ? tile[tx][j] / scale[blockIdx.z] : tile[tx][j];
+    }
+  } else {
+    for (int j = ty; j < 32; j += 8) {
+      const int c = c0 + j, r = r0 + tx;
+      if (r < R && c < C) d[(int64_t)c * R + r] = scale ? s[(int64_t)c * R + r] / scale[blockIdx.z] : s[(int64_t)c * R + r];
+    }
+  }
+}
+
+struct PolarLayout {
+  size_t X, Y, A, B, scale, total;
+};
+
+PolarLayout polar_layout(const fc_polar_desc& d) {
+  const size_t lo = std::min(d.m, d.n), hi = std::max(d.m, d.n), k = d.count;
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  PolarLayout L{};
+  L.X = 0;
+  L.Y = L.X + up(lo * hi * k * 4);
+  L.A = L.Y + up(lo * hi * k * 4);
+  L.B = L.A + up(lo * lo * k * 4);
+  L.scale = L.B + up(lo * lo * k * 4);
+  L.total = L.scale + up(k * 4);
+  return L;
+}
+
+// (a, b, c) of each step (src/optim.jl:97-103), as the reference's Float32 literals.
+constexpr float kPolar[5][3] = {
+    {8.156554524902461f, -22.48329292557795f, 15.878769915207462f},
+    {4.042929935166739f, -2.808917465908714f, 0.5000178451051316f},
+    {3.8916678022926607f, -2.772484153217685f, 0.5060648178503393f},
+    {3.285753657755655f, -2.3681294933425376f, 0.46449024233003106f},
+    {2.3465413258596377f, -1.7097828382687081f, 0.42323551169305323f},
+};
+
+// One rocBLAS handle per device, created on first use (it allocates its own
+// workspace then) and used under a lock.
+std::mutex g_blas_mutex;
+rocblas_handle g_blas[16] = {};
+
+rocblas_handle blas_handle(int dev) {
+  rocblas_handle& h = g_blas[dev & 15];
+  if (h == nullptr && rocblas_create_handle(&h) != rocblas_status_success) h = nullptr;
+  return h;
+}
+
+rocblas_status gemm(rocblas_handle h, rocblas_operation ta, rocblas_operation tb, int m, int n, int k, float alpha,
+                    const float* A, int lda, int64_t sa, const float* B, int ldb, int64_t sb, float beta,
+                    const float* C, int ldc, int64_t sc, float* D, int batch) {
+  return rocblas_gemm_strided_batched_ex(h, ta, tb, m, n, k, &alpha, A, rocblas_datatype_f32_r, lda, sa, B,
+                                         rocblas_datatype_f32_r, ldb, sb, &beta, C, rocblas_datatype_f32_r, ldc, sc,
+                                         D, rocblas_datatype_f32_r, ldc, sc, batch, rocblas_datatype_f32_r,
+                                         rocblas_gemm_algo_standard, 0, 0);
+}
+
+}  // namespace
+}  // namespace fc
+
+using namespace fc;
+
+extern "C" {
+
+fc_status fc_adamw_step(const fc_adamw_desc* d, float* theta, const float* grad, float* m, float* v, void* stream) {
+  if (d == nullptr) return failf(FC_ERR_INVALID_ARGUMENT, "fc_adamw_step: descriptor is null");
+  if (d->n <= 0 || d->t < 1)
+    return failf(FC_ERR_INVALID_ARGUMENT, "fc_adamw_step: n must be positive and t >= 1 (n=%lld t=%d)",
+                 (long long)d->n, d->t);
+  if (!theta || !grad || !m || !v) return failf(FC_ERR_INVALID_ARGUMENT, "fc_adamw_step: a pointer is null");
+  if (((reinterpret_cast<uintptr_t>(theta) | reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(m) |
+        reinterpret_cast<uintptr_t>(v)) & 3) != 0)
+    return failf(FC_ERR_INVALID_ARGUMENT, "fc_adamw_step: arrays must be 4-byte aligned");
+  AdamScalars s;
+  s.b1 = d->beta1;
+  s.omb1 = 1.0f - d->beta1;
+  s.b2 = d->beta2;
+  s.omb2 = 1.0f - d->beta2;
+  s.decay = 1.0f - d->alpha * d->lambda;
+  s.c1 = 1.0f - julia_pow(d->beta1, d->t);
+  s.c2 = 1.0f - julia_pow(d->beta2, d->t);
+  s.alpha = d->alpha;
+  s.eps = d->eps;
+  s.nscale = d->grad_scale;
+  const bool vec = aligned16(theta) && aligned16(grad) && aligned16(m) && aligned16(v);
+  hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(vec ? d->n / 4 : d->n)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), d->n, theta, grad, m, v, s, vec);
+  return launched("AdamW");
+}
+
+fc_status fc_adam_update(int64_t n, int64_t offset, float lambda, float eps, float* Theta, const float* m,
+                         const float* v, const float* alpha, const float* beta, const float* eta, void* stream) {
+  if (n <= 0 || offset < 0) return failf(FC_ERR_INVALID_ARGUMENT, "fc_adam_update: n must be positive, offset >= 0");
+  if (!Theta || !m || !v || !alpha || !beta || !eta)
+    return failf(FC_ERR_INVALID_ARGUMENT, "fc_adam_update: a pointer is null");
+  hipLaunchKernelGGL(adam_update_kernel, dim3(grid_for(n)), dim3(256), 0, static_cast<hipStream_t>(stream), n,
+                     Theta + offset, m, v, alpha, beta, eta, lambda, eps);
+  return launched("Adam update");
+}
+
+fc_status fc_muon_update(int64_t width, int32_t count, float* Theta, const float* X, const float* eta,
+                         const float* lambda, const int64_t* offsets, void* stream) {
+  if (width <= 0 || count <= 0 || count > 65535)
+    return failf(FC_ERR_INVALID_ARGUMENT, "fc_muon_update: width must be positive and count in [1, 65535]");
+  if (!Theta || !X || !eta || !lambda || !offsets) return failf(FC_ERR_INVALID_ARGUMENT, "fc_muon_update: a pointer is null");
+  hipLaunchKernelGGL(muon_kernel, dim3(grid_for((width + 3) / 4, 256, 4096), count), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), width, Theta, X, eta, lambda, offsets);
+  return launched("Muon update");
+}
+
+static fc_status param_copy(bool gather, int64_t width, int32_t count, float* stack, float* vector,
+                            const int64_t* offsets, void* stream) {
+  if (width <= 0 || count <= 0 || count > 65535)
+    return failf(FC_ERR_INVALID_ARGUMENT, "parameter copy: width must be positive and count in [1, 65535]");
+  if (!stack || !vector || !offsets) return failf(FC_ERR_INVALID_ARGUMENT, "parameter copy: a pointer is null");
+  const dim3 grid(grid_for((width + 3) / 4, 256, 4096), count);
+  if (gather) hipLaunchKernelGGL(param_copy_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), width, stack, vector, offsets);
+  else hipLaunchKernelGGL(param_copy_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), width, stack, vector, offsets);
+  return launched(gather ? "gather" : "scatter");
+}
+
+fc_status fc_param_gather(int64_t width, int32_t count, float* stack, const float* vector, const int64_t* offsets,
+                          void* stream) {
+  return param_copy(true, width, count, stack, const_cast<float*>(vector), offsets, stream);
+}
+
+fc_status fc_param_scatter(int64_t width, int32_t count, float* vector, const float* stack, const int64_t* offsets,
+                           void* stream) {
+  return param_copy(false, width, count, const_cast<float*>(stack), vector, offsets, stream);
+}
+
+static fc_status polar_check(const fc_polar_desc* d) {
+  if (d == nullptr) return failf(FC_ERR_INVALID_ARGUMENT, "polar express: descriptor is null");
+  if (d->m <= 0 || d->n <= 0 || d->count <= 0 || d->steps < 0)
+    return failf(FC_ERR_INVALID_ARGUMENT, "polar express: sizes must be positive (m=%d n=%d count=%d steps=%d)", d->m,
+                 d->n, d->count, d->steps);
+  if (d->count > 65535) return failf(FC_ERR_UNSUPPORTED, "polar express: at most 65535 matrices");
+  if (d->dtype != FC_F32) return failf(FC_ERR_UNSUPPORTED, "polar express: only the FC_F32 compute type is built");
+  return FC_OK;
+}
+
+fc_status fc_polar_workspace_bytes(const fc_polar_desc* d, size_t* bytes) {
+  const fc_status st = polar_check(d);
+  if (st != FC_OK) return st;
+  if (bytes == nullptr) return failf(FC_ERR_INVALID_ARGUMENT, "polar express: bytes is null");
+  *bytes = polar_layout(*d).total;
+  clear_error();
+  return FC_OK;
+}
+
+fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, void* stream) {
+  fc_status st = polar_check(d);
+  if (st != FC_OK) return st;
+  if (G == nullptr) return failf(FC_ERR_INVALID_ARGUMENT, "polar express: G is null");
+  const PolarLayout L = polar_layout(*d);
+  if (workspace == nullptr || workspace_bytes < L.total)
+    return failf(FC_ERR_WORKSPACE, "polar express needs %zu workspace bytes, got %zu", L.total, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return failf(FC_ERR_WORKSPACE, "polar express: workspace must be 256-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  float* X = reinterpret_cast<float*>(ws + L.X);
+  float* Y = reinterpret_cast<float*>(ws + L.Y);
+  float* A = reinterpret_cast<float*>(ws + L.A);
+  float* B = reinterpret_cast<float*>(ws + L.B);
+  float* scale = reinterpret_cast<float*>(ws + L.scale);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int m = d->m, n = d->n, k = d->count;
+  const bool transposed = m > n;
+  const int lo = std::min(m, n), hi = std::max(m, n);
+  const int64_t sx = (int64_t)lo * hi, sa = (int64_t)lo * lo;
+
+  hipLaunchKernelGGL(frobenius_kernel, dim3(k), dim3(1024), 0, s, (int64_t)m * n, G, scale);
+  if ((st = launched("polar norm")) != FC_OK) return st;
+  // X (lo x hi) = G / scale, or G^T / scale
+  const dim3 tiles((lo + 31) / 32, (hi + 31) / 32, k);
+  if (transposed) hipLaunchKernelGGL(copy_scaled_kernel<true>, tiles, dim3(256), 0, s, lo, hi, G, X, scale);
+  else hipLaunchKernelGGL(copy_scaled_kernel<false>, tiles, dim3(256), 0, s, lo, hi, G, X, scale);
+  if ((st = launched("polar copy in")) != FC_OK) return st;
+
+  int dev = 0;
+  hipGetDevice(&dev);
+  {
+    std::lock_guard<std::mutex> lock(g_blas_mutex);
+    rocblas_handle h = blas_handle(dev);
+    if (h == nullptr) return failf(FC_ERR_HIP, "polar express: rocblas_create_handle failed");
+    if (rocblas_set_stream(h, s) != rocblas_status_success) return failf(FC_ERR_HIP, "rocblas_set_stream failed");
+    const auto N = rocblas_operation_none, T = rocblas_operation_transpose;
+    for (int t = 0; t < d->steps; ++t) {
+      const float* c = kPolar[std::min(t, 4)];
+      rocblas_status r;
+      // A = X X^T
+      r = gemm(h, N, T, lo, lo, hi, 1.0f, X, lo, sx, X, lo, sx, 0.0f, A, lo, sa, A, k);
+      // B = c A A + b A
+      if (r == rocblas_status_success) r = gemm(h, N, N, lo, lo, lo, c[2], A, lo, sa, A, lo, sa, c[1], A, lo, sa, B, k);
+      // Y = B X + a X, then X <-> Y
+      if (r == rocblas_status_success) r = gemm(h, N, N, lo, hi, lo, 1.0f, B, lo, sa, X, lo, sx, c[0], X, lo, sx, Y, k);
+      if (r != rocblas_status_success) return failf(FC_ERR_HIP, "polar express: rocBLAS GEMM failed (%d)", (int)r);
+      std::swap(X, Y);
+    }
+  }
+  // G = X, or X^T
+  if (transposed) hipLaunchKernelGGL(copy_scaled_kernel<true>, dim3((hi + 31) / 32, (lo + 31) / 32, k), dim3(256), 0, s, hi, lo, X, G, nullptr);
+  else hipLaunchKernelGGL(copy_scaled_kernel<false>, tiles, dim3(256), 0, s, lo, hi, X, G, nullptr);
+  return launched("polar copy out");
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+"""GPU parity of the optimizer kernels against oracle/optim.py.
+
+The elementwise updates (AdamW step, CUDA Adam/Muon final writes,
+gather/scatter) run the reference's fp32 operations in its order without
+contraction, so they must equal the float32 oracle bit for bit, on both the
+16-byte path and the scalar tail.  Polar Express runs fp32 batched GEMMs
+(rocBLAS) through five polynomial steps whose coefficients reach 22, which
+could amplify rounding in the smallest singular directions: it is compared
+with the float64 oracle and with the same iteration in plain torch fp32
+within the fp32 contract's 1e-4 (measured: about 1e-5 at 512 x 2048).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from femtochat_amd import AdamW, adam_update_, gather_, muon_update_, polar_express, scatter_
+from oracle import optim as O
+
+from tests.helpers import rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+# Polar Express: max |X - R| / max |R| against float64, and against torch fp32
+POLAR_TOL = 1e-4
+
+
+@pytest.mark.parametrize("n,misalign", [(1_000_003, 0), (4096, 1), (7, 0)])
+def test_adamw_steps_are_bit_exact(gpu, n, misalign):
+    g = torch.Generator().manual_seed(n)
+    theta = torch.randn(n + misalign, generator=g)
+    dev_theta = theta.to(gpu)[misalign:]  # misalign = 1: 4-byte offset, the scalar path
+    opt = AdamW(dev_theta, alpha=0.02, beta1=0.8, beta2=0.95, eps=1e-10, lam=0.01)
+    th, m, v = theta[misalign:].numpy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for t in range(1, 5):
+        grad = torch.randn(n, generator=g) * (0.1 * t)
+        gbuf = torch.zeros(n + misalign)
+        gbuf[misalign:] = grad
+        opt(dev_theta, gbuf.to(gpu)[misalign:], grad_scale=2.0 if t == 3 else 1.0)
+        th, m, v = O.adamw_step(th, grad.numpy(), m, v, t, 0.02, 0.8, 0.95, 1e-10, 0.01,
+                                grad_scale=2.0 if t == 3 else 1.0)
+    assert np.array_equal(dev_theta.cpu().numpy(), th)
+    assert np.array_equal(opt.m.cpu().numpy(), m) and np.array_equal(opt.v.cpu().numpy(), v)
+
+
+def test_adam_update_is_bit_exact(gpu):
+    g = torch.Generator().manual_seed(1)
+    Th = torch.randn(5000, generator=g)
+    m, v = torch.randn(3000, generator=g), torch.rand(3000, generator=g)
+    scal = [torch.tensor([x], device=gpu) for x in (0.05, 0.3, 0.01)]
+    Td = Th.to(gpu)
+    adam_update_(Td, 1234, m.to(gpu), v.to(gpu), *scal, lam=0.1, eps=1e-8)
+    ref = O.adam_update(Th.numpy(), 1234, m.numpy(), v.numpy(), 0.05, 0.3, 0.01, 0.1, 1e-8)
+    assert np.array_equal(Td.cpu().numpy(), ref)
+
+
+def test_muon_update_gather_scatter_are_bit_exact(gpu):
+    g = torch.Generator().manual_seed(2)
+    width, count = 48 * 32, 5
+    Th = torch.randn(20000, generator=g)
+    Th[::17] = 0.0  # zero parameters: x * theta = 0 takes the decay branch
+    offsets = torch.tensor([0, 3000, 7000, 11111, 15000], dtype=torch.int64)
+    X = torch.randn(count, width, generator=g)
+    X[:, ::13] = 0.0
+    Td = Th.to(gpu)
+    muon_update_(Td, X.to(gpu), torch.tensor([0.02], device=gpu), torch.tensor([0.1], device=gpu), offsets.to(gpu))
+    ref = O.muon_update(Th.numpy(), X.numpy(), offsets.numpy(), 0.02, 0.1)
+    assert np.array_equal(Td.cpu().numpy(), ref)
+    stack = torch.empty(count, width, device=gpu)
+    gather_(stack, Td, offsets.to(gpu))
+    assert np.array_equal(stack.cpu().numpy(), O.gather(ref, offsets.numpy(), width))
+    out = torch.zeros(20000, device=gpu)
+    scatter_(out, stack * 2, offsets.to(gpu))
+    assert np.array_equal(out.cpu().numpy(), O.scatter(np.zeros(20000, np.float32), O.gather(ref, offsets.numpy(), width) * 2,
+                                                       offsets.numpy()))
+
+
+def _torch_polar_f32(G):
+    """The same iteration in plain torch fp32 (Julia (m, n) = torch (n, m) per matrix)."""
+    out = []
+    for g in G:  # g: torch (n, m) = G_j^T
+        M = g.T  # (m, n)
+        transposed = M.shape[0] > M.shape[1]
+        X = (M.T if transposed else M) / (np.float32(1.01) * torch.sqrt((M * M).sum()) + np.float32(1e-6))
+        for a, b, c in O.COEFFICIENTS:
+            A = X @ X.T.contiguous()
+            B = np.float32(b) * A + np.float32(c) * (A @ A)
+            X = np.float32(a) * X + B @ X
+        out.append((X.T if transposed else X).T)
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 3), (48, 160, 2), (160, 48, 2), (512, 2048, 1), (2048, 512, 1)])
+def test_polar_express_matches_oracle(gpu, m, n, k):
+    g = torch.Generator().manual_seed(m * 7 + n)
+    G = torch.randn(k, n, m, generator=g)  # Julia (m, n, k)
+    out = polar_express(G.to(gpu)).cpu()
+    julia = G.numpy().transpose(0, 2, 1)  # [j] = Julia G[:, :, j] (m, n)
+    ref = O.polar_express(julia).transpose(0, 2, 1)
+    e64 = rel_err(out.numpy(), ref)
+    e32 = rel_err(out.numpy(), _torch_polar_f32(G.to(gpu)).cpu().numpy())
+    say(f"polar {m}x{n}x{k}: vs float64 {e64:.2e}, vs torch fp32 {e32:.2e}")
+    assert e64 < POLAR_TOL and e32 < POLAR_TOL
+    # the output's singular values are the composed polynomial of the normalised input's
+    for j in range(k):
+        s_in = np.linalg.svd(julia[j].astype(np.float64), compute_uv=False)
+        scale = float(np.float32(1.01)) * np.sqrt(np.sum(julia[j].astype(np.float64) ** 2)) + float(np.float32(1e-6))
+        s_out = np.linalg.svd(out[j].numpy().astype(np.float64), compute_uv=False)
+        np.testing.assert_allclose(np.sort(s_out), np.sort(O.composed_polynomial(s_in / scale)), atol=POLAR_TOL * 4)

@@ -281,6 +281,9 @@ def main() -> int:
     ap.add_argument("--workload", default="C3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=16, help="batch rows in the CPU baseline sample")
+    ap.add_argument("--sections", default="prologue,loss,optim",
+                    help="measurements besides the headline attention step (comma list of prologue, loss, optim; "
+                         "'none' for only the headline)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this build has a single MI355X, and the attention "
@@ -359,9 +362,10 @@ def main() -> int:
             rec["hbm_bytes"] = traffic[key]
             rec["hbm_gbs"] = round(traffic[key] / (rec["avg_ms"] * 1e-3) / 1e9, 1)
 
-    prologue = measure_prologue(wl, dev, args.steps) if fast else None
-    loss_side = measure_loss(dev, args.steps) if fast else None
-    optim_side = measure_optim(dev, args.steps) if fast else None
+    sections = set(args.sections.split(",")) if fast else set()
+    prologue = measure_prologue(wl, dev, args.steps) if "prologue" in sections else None
+    loss_side = measure_loss(dev, args.steps) if "loss" in sections else None
+    optim_side = measure_optim(dev, args.steps) if "optim" in sections else None
 
     cpu = None
     if not args.no_cpu:

@@ -8,7 +8,7 @@
 // accesses where the sizes allow, a scalar tail otherwise.
 //
 // Polar Express (src/optim.jl:115-149) normalises each matrix by its
-// Frobenius norm (one workgroup per matrix), copies it into the iteration
+// Frobenius norm (a two-stage float64 reduction), copies it into the iteration
 // buffer (transposed through LDS when m > n, so the Gram matrix is the
 // smaller one), runs three strided-batched rocBLAS GEMMs per step with the
 // elementwise terms folded into their beta, and copies the result back.
@@ -163,21 +163,31 @@ __global__ __launch_bounds__(256) void param_copy_kernel(int64_t width, float* s
 }
 
 // ---- Polar Express -------------------------------------------------------------------
-// scale[k] = 1.01 sqrt(sum G_k^2) + 1e-6 (sum in float64).
-__global__ __launch_bounds__(1024) void frobenius_kernel(int64_t size, const float* G, float* scale) {
-  __shared__ double part[16];
-  const float* g = G + (int64_t)blockIdx.x * size;
+// scale[k] = 1.01 sqrt(sum G_k^2) + 1e-6, summed in float64 in two stages
+// (kNormParts workgroups per matrix write partial sums, then one workgroup
+// per matrix adds them in a fixed order: deterministic).
+constexpr int kNormParts = 64;
+
+__global__ __launch_bounds__(256) void norm_partial_kernel(int64_t size, const float* G, double* partial) {
+  __shared__ double part[4];
+  const int k = blockIdx.y;
+  const float* g = G + (int64_t)k * size;
   double s = 0.0;
-  for (int64_t i = threadIdx.x; i < size; i += 1024) s += (double)g[i] * (double)g[i];
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < size; i += (int64_t)kNormParts * 256)
+    s += (double)g[i] * (double)g[i];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = s;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (int w = 0; w < 16; ++w) t += part[w];
-    scale[blockIdx.x] = 1.01f * sqrtf((float)t) + 1e-6f;
-  }
+  if (threadIdx.x == 0) partial[k * kNormParts + blockIdx.x] = ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+__global__ __launch_bounds__(64) void norm_finish_kernel(const double* partial, float* scale) {
+  const int k = blockIdx.x;
+  double s = partial[k * kNormParts + threadIdx.x];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  if (threadIdx.x == 0) scale[k] = 1.01f * sqrtf((float)s) + 1e-6f;
 }
 
 // dst (rows R, cols C, column-major) = src^T / scale (src: C rows, R cols) or
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const fl
 }
 
 struct PolarLayout {
-  size_t X, Y, A, B, scale, total;
+  size_t X, Y, A, B, scale, partial, total;
 };
 
 PolarLayout polar_layout(const fc_polar_desc& d) {
@@ -223,7 +233,8 @@ PolarLayout polar_layout(const fc_polar_desc& d) {
   L.A = L.Y + up(lo * hi * k * 4);
   L.B = L.A + up(lo * lo * k * 4);
   L.scale = L.B + up(lo * lo * k * 4);
-  L.total = L.scale + up(k * 4);
+  L.partial = L.scale + up(k * 4);
+  L.total = L.partial + up(k * kNormParts * 8);
   return L;
 }
 
@@ -364,13 +375,16 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
   float* A = reinterpret_cast<float*>(ws + L.A);
   float* B = reinterpret_cast<float*>(ws + L.B);
   float* scale = reinterpret_cast<float*>(ws + L.scale);
+  double* partial = reinterpret_cast<double*>(ws + L.partial);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int m = d->m, n = d->n, k = d->count;
   const bool transposed = m > n;
   const int lo = std::min(m, n), hi = std::max(m, n);
   const int64_t sx = (int64_t)lo * hi, sa = (int64_t)lo * lo;
 
-  hipLaunchKernelGGL(frobenius_kernel, dim3(k), dim3(1024), 0, s, (int64_t)m * n, G, scale);
+  hipLaunchKernelGGL(norm_partial_kernel, dim3(kNormParts, k), dim3(256), 0, s, (int64_t)m * n, G, partial);
+  if ((st = launched("polar norm")) != FC_OK) return st;
+  hipLaunchKernelGGL(norm_finish_kernel, dim3(k), dim3(64), 0, s, partial, scale);
   if ((st = launched("polar norm")) != FC_OK) return st;
   // X (lo x hi) = G / scale, or G^T / scale
   const dim3 tiles((lo + 31) / 32, (hi + 31) / 32, k);

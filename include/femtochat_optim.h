@@ -68,7 +68,8 @@ typedef struct {
 } fc_polar_desc;
 
 /* Bytes of the caller-owned workspace of fc_polar_express (X, Y, A, B and
-   the per-matrix scale, as the reference's polar_workspace). */
+   the per-matrix scale, as the reference's polar_workspace, plus 512 bytes
+   per matrix of partial sums for the norm). */
 fc_status fc_polar_workspace_bytes(const fc_polar_desc* desc, size_t* bytes);
 
 /* Polar Express in place on G (m, n, count) float32 (reference

@@ -149,13 +149,15 @@ def measure_loss(dev, steps: int) -> dict:
     """Loss-side kernels at the training step's shape (scripts/train.jl
     defaults: vocabulary 2^15, 4 x 2048 tokens, 512-wide embeddings; fp32
     logits and weights): cross-entropy forward (losses, log-sum-exp, mean),
-    its gradient accumulating into the logits' gradient, the embedding gather
+    its gradient accumulating into the logits' gradient, both in one pass
+    (fused, writing the gradient), the embedding gather
     and its scatter-add gradient.  HBM-bound: algorithmic bytes per unit time
     against 8 TB/s.  Not part of the headline value."""
     import torch
 
     import femtochat_amd._lib as L
-    from femtochat_amd import cross_entropy_, cross_entropy_gradient_, embedding_, embedding_gradient_
+    from femtochat_amd import (cross_entropy_, cross_entropy_fused_, cross_entropy_gradient_, embedding_,
+                               embedding_gradient_)
 
     V, N, D = 32768, 4 * 2048, 512
     g = torch.Generator(device=dev).manual_seed(0)
@@ -174,6 +176,7 @@ def measure_loss(dev, steps: int) -> dict:
     def once():
         cross_entropy_(losses, logits, targets, -1, "mean", lse=lse, reduced=reduced, count=count)
         cross_entropy_gradient_(dlogits, logits, targets, dy, -1, "mean", lse=lse, count=count)
+        cross_entropy_fused_(losses, dlogits, logits, targets, dy, -1, "mean", lse=lse, count=count)
         embedding_(y, W, tokens)
         embedding_gradient_(dW, dY, tokens)
 
@@ -190,8 +193,10 @@ def measure_loss(dev, steps: int) -> dict:
     lg, em = N * V * 4, N * D * 4
     out = {"workload": f"train.jl step: V={V}, N={N} tokens (B=4, T=2048), D={D}, fp32; uniform random targets/tokens"}
     # bytes per launch: logits read; logits read + gradient read and written;
-    # weight rows read + output written; dy read + weight rows read and written
-    for name, nbytes in (("xent_fwd", lg), ("xent_bwd", 3 * lg), ("embed_fwd", 2 * em), ("embed_bwd", 3 * em)):
+    # fused: logits read + gradient written; weight rows read + output written;
+    # dy read + weight rows read and written
+    for name, nbytes in (("xent_fwd", lg), ("xent_bwd", 3 * lg), ("xent_fused", 2 * lg), ("embed_fwd", 2 * em),
+                         ("embed_bwd", 3 * em)):
         n, tot = k[name]
         ms = tot / steps
         achieved = nbytes / (ms * 1e-3) / 1e9

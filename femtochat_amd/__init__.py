@@ -37,6 +37,7 @@ from .loss import (  # noqa: F401
     EmbeddingFunction,
     cross_entropy,
     cross_entropy_,
+    cross_entropy_fused_,
     cross_entropy_gradient_,
     embedding,
     embedding_,

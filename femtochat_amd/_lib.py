@@ -176,6 +176,7 @@ _SIGNATURES = {
     "fc_cross_entropy_fwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P]),
     "fc_cross_entropy_count": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P]),
     "fc_cross_entropy_bwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P]),
+    "fc_cross_entropy_fused": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "fc_embedding_fwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
     "fc_embedding_bwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
     "fc_xla_bind_attention_fwd": (ctypes.c_void_p, [ctypes.POINTER(AttnDesc), ctypes.c_int32]),

@@ -447,6 +447,34 @@ fc_status fc_cross_entropy_bwd(const fc_xent_desc* desc, float* dlogits, const f
   return ok();
 }
 
+fc_status fc_cross_entropy_fused(const fc_xent_desc* desc, const float* logits, const void* targets, float* losses,
+                                 float* lse, float* reduced, float* dlogits, const float* dy, const float* count,
+                                 void* stream) {
+  fc::XentArgs a;
+  const fc_status st = xent_args(desc, targets, "fc_cross_entropy_fused", &a);
+  if (st != FC_OK) return st;
+  if (logits == nullptr || losses == nullptr || dlogits == nullptr || dy == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_fused: logits, losses, dlogits and dy are required");
+  if (desc->reduction == FC_REDUCE_MEAN && count == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_fused: the mean gradient needs the valid-target count");
+  if (!aligned4(losses) || !aligned4(lse) || !aligned4(reduced) || !aligned4(dy) || !aligned4(count))
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_cross_entropy_fused: float buffers must be 4-byte aligned");
+  a.logits = logits;
+  a.losses = losses;
+  a.lse = lse;
+  a.reduced = reduced;
+  a.dlogits = dlogits;
+  a.dy = dy;
+  a.count = const_cast<float*>(count);
+  if (!fc::xent_fused_supported(a))
+    return fail(FC_ERR_UNSUPPORTED,
+                "fc_cross_entropy_fused: needs V a multiple of 4, V <= 32768 and 16-byte aligned logits and dlogits "
+                "(use fc_cross_entropy_fwd and fc_cross_entropy_bwd)");
+  const hipError_t e = fc::launch_xent_fused(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "fused cross-entropy launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 static fc_status embed_args(const fc_embed_desc* d, const void* tokens, const char* who, fc::EmbedArgs* a) {
   if (d == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "%s: descriptor is null", who);
   if (d->D <= 0 || d->vocab <= 0 || d->N <= 0)

@@ -137,6 +137,8 @@ struct XentArgs {
 hipError_t launch_xent_fwd(const XentArgs& a, hipStream_t s);
 hipError_t launch_xent_count(const XentArgs& a, hipStream_t s);
 hipError_t launch_xent_bwd(const XentArgs& a, hipStream_t s);
+bool xent_fused_supported(const XentArgs& a);
+hipError_t launch_xent_fused(const XentArgs& a, hipStream_t s);
 
 // Embedding gather and scatter-add (loss.hip).
 struct EmbedArgs {

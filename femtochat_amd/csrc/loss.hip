@@ -204,6 +204,75 @@ __global__ __launch_bounds__(256) void xent_bwd_kernel(XentArgs a) {
   }
 }
 
+// ---- fused forward and gradient ------------------------------------------------
+// One 1024-thread workgroup per token holds the whole column in registers
+// (up to kFusedChunks 16-byte chunks per thread: V <= 4096 kFusedChunks),
+// so the logits are read once: maximum, sum of exponentials, the loss, and
+// the gradient scale (p - onehot) written (or added) in the same pass.
+constexpr int kFusedChunks = 8;
+constexpr int kFusedThreads = 1024;
+
+__device__ inline float block_reduce_1024(float v, bool is_max, float* slots) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float u = __shfl_xor(v, o);
+    v = is_max ? fmaxf(v, u) : v + u;
+  }
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x / 64] = v;
+  __syncthreads();
+  float r = slots[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) r = is_max ? fmaxf(r, slots[w]) : r + slots[w];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kFusedThreads) void xent_fused_kernel(XentArgs a) {
+  __shared__ float slots[16];
+  const int64_t token = blockIdx.x;
+  const float* col = a.logits + token * (int64_t)a.V;
+  float* out = a.dlogits + token * (int64_t)a.V;
+  const int chunks = a.V / 4;
+  f32x4 x[kFusedChunks];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kFusedChunks; ++k) {
+    const int c = threadIdx.x + kFusedThreads * k;
+    x[k] = c < chunks ? *reinterpret_cast<const f32x4*>(col + 4 * c) : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    mx = fmaxf(mx, fmaxf(fmaxf(x[k][0], x[k][1]), fmaxf(x[k][2], x[k][3])));
+  }
+  const float M = block_reduce_1024(mx, true, slots);
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum += exp2f((x[k][i] - M) * kLog2e);
+  const float lse = M + logf(block_reduce_1024(sum, false, slots));
+  const int64_t raw = index_at(a.targets, token, a.index_type);
+  const int64_t t = raw - a.index_base;
+  const bool valid = raw != a.ignore_index;
+  if (threadIdx.x == 0) {
+    a.losses[token] = valid ? ((t >= 0 && t < a.V) ? lse - col[t] : __builtin_nanf("")) : 0.0f;
+    if (a.lse != nullptr) a.lse[token] = lse;
+  }
+  if (!valid) return;  // uniform: the gradient column is left untouched, as the separate gradient does
+  float w = a.dy[a.reduction == 0 ? token : 0];
+  if (a.reduction == 2) w = w / *a.count;
+#pragma unroll
+  for (int k = 0; k < kFusedChunks; ++k) {
+    const int c = threadIdx.x + kFusedThreads * k;
+    if (c >= chunks) continue;
+    f32x4 g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = exp2f((x[k][i] - lse) * kLog2e);
+      g[i] = w * (p - (4 * c + i == t ? 1.0f : 0.0f));
+    }
+    f32x4* o = reinterpret_cast<f32x4*>(out + 4 * c);
+    *o = a.overwrite ? g : *o + g;
+  }
+}
+
 // ---- embedding ----------------------------------------------------------------
 // One wave per token, 16-byte chunks of its column (D % 4 == 0) or scalars.
 template <bool kVec, typename Y>
@@ -276,6 +345,21 @@ hipError_t launch_xent_fwd(const XentArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_xent_count(const XentArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(xent_reduce_kernel, dim3(1), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+bool xent_fused_supported(const XentArgs& a) {
+  return a.V % 4 == 0 && a.V <= 4 * kFusedThreads * kFusedChunks &&
+         ((reinterpret_cast<uintptr_t>(a.logits) | reinterpret_cast<uintptr_t>(a.dlogits)) & 15) == 0;
+}
+
+hipError_t launch_xent_fused(const XentArgs& a, hipStream_t s) {
+  const ProfileMark mk = profile_begin(s);
+  hipLaunchKernelGGL(xent_fused_kernel, dim3((unsigned)a.N), dim3(kFusedThreads), 0, s, a);
+  hipError_t e = hipGetLastError();
+  profile_end(mk, "xent_fused", s);
+  if (e != hipSuccess || (a.reduced == nullptr)) return e;
   hipLaunchKernelGGL(xent_reduce_kernel, dim3(1), dim3(1024), 0, s, a);
   return hipGetLastError();
 }

@@ -33,6 +33,7 @@ __all__ = [
     "cross_entropy",
     "cross_entropy_",
     "cross_entropy_gradient_",
+    "cross_entropy_fused_",
     "valid_target_count",
     "CrossEntropyFunction",
     "embedding",
@@ -136,6 +137,32 @@ def cross_entropy_gradient_(delta: torch.Tensor, logits: torch.Tensor, targets: 
         count = valid_target_count(targets, ignore_index)
     _lib.check(_lib.lib().fc_cross_entropy_bwd(ctypes.byref(d), _ptr(delta), _ptr(logits), _ptr(targets), _ptr(dy),
                                                _ptr(count), _ptr(lse), _stream_ptr(dev)))
+
+
+def cross_entropy_fused_(losses: torch.Tensor, delta: torch.Tensor, logits: torch.Tensor, targets: torch.Tensor,
+                         dy=1.0, ignore_index: int = -1, reduction: str = "mean", *, index_base: int = 0,
+                         lse: Optional[torch.Tensor] = None, reduced: Optional[torch.Tensor] = None,
+                         count: Optional[torch.Tensor] = None, accumulate: bool = False) -> None:
+    """The losses and the gradient in one pass over the logits (the loss as
+    the step's last node): ``cross_entropy_`` then ``cross_entropy_gradient_``
+    with the logits read once.  Needs a vocabulary that is a multiple of 4 and
+    at most 32768 (the library raises FC_ERR_UNSUPPORTED otherwise)."""
+    d = _xent_desc(logits, targets, ignore_index, reduction, index_base, overwrite=not accumulate)
+    dev = logits.device
+    _check_tensor("losses", losses, tuple(targets.shape), (torch.float32,), dev)
+    _check_tensor("delta", delta, tuple(logits.shape), (torch.float32,), dev)
+    if not isinstance(dy, torch.Tensor):
+        dy = torch.full((1,), float(dy), dtype=torch.float32, device=dev)
+    dy = dy.to(device=dev, dtype=torch.float32).contiguous()
+    if dy.numel() != (targets.numel() if reduction == "none" else 1):
+        raise ValueError(f"dy has the wrong number of values for reduction {reduction!r}")
+    for name, t, shape in (("lse", lse, tuple(targets.shape)), ("reduced", reduced, (1,)), ("count", count, (1,))):
+        if t is not None:
+            _check_tensor(name, t, shape, (torch.float32,), dev)
+    if reduction == "mean" and count is None:
+        count = valid_target_count(targets, ignore_index)
+    _lib.check(_lib.lib().fc_cross_entropy_fused(ctypes.byref(d), _ptr(logits), _ptr(targets), _ptr(losses), _ptr(lse),
+                                                 _ptr(reduced), _ptr(delta), _ptr(dy), _ptr(count), _stream_ptr(dev)))
 
 
 class CrossEntropyFunction(torch.autograd.Function):

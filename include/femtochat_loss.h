@@ -61,6 +61,20 @@ fc_status fc_cross_entropy_count(const fc_xent_desc* desc, const void* targets, 
 fc_status fc_cross_entropy_bwd(const fc_xent_desc* desc, float* dlogits, const float* logits, const void* targets,
                                const float* dy, const float* count, const float* lse, void* stream);
 
+/* Forward and gradient in one pass over the logits, for the loss as the last
+   node of the step: the losses (and optionally lse and the reduced value, as
+   fc_cross_entropy_fwd) and dlogits += (or, with FC_FLAG_OVERWRITE, =)
+   scale * (softmax(x) - onehot(target)) with scale from dy and count as
+   fc_cross_entropy_bwd (count from fc_cross_entropy_count for the mean).
+   One workgroup holds a token's column in registers: V a multiple of 4 and
+   at most 32768, logits and dlogits 16-byte aligned (FC_ERR_UNSUPPORTED
+   otherwise).  No reference counterpart as one call: it is the reference's
+   cross_entropy then cross_entropy_gradient! (src/gpt.jl:175-195,
+   src/kernels.jl:16-28) with the logits read once instead of twice or three times. */
+fc_status fc_cross_entropy_fused(const fc_xent_desc* desc, const float* logits, const void* targets, float* losses,
+                                 float* lse, float* reduced, float* dlogits, const float* dy, const float* count,
+                                 void* stream);
+
 typedef struct {
   int32_t D;          /* embedding width: length of a weight column */
   int32_t vocab;      /* number of weight columns */

@@ -17,7 +17,9 @@ import torch
 import torch.nn.functional as F
 
 from femtochat_amd import (CrossEntropyFunction, EmbeddingFunction, cross_entropy, cross_entropy_,
-                           cross_entropy_gradient_, embedding, embedding_gradient_, valid_target_count)
+                           cross_entropy_fused_, cross_entropy_gradient_, embedding, embedding_gradient_,
+                           valid_target_count)
+from femtochat_amd import _lib
 from oracle import loss as O
 
 from tests.helpers import rel_err, say
@@ -103,6 +105,45 @@ def test_gradient_matches_oracle(gpu, V, reduction, with_lse):
     cross_entropy_gradient_(delta2, xd, td, dy.to(gpu), -1, reduction, lse=lse, accumulate=False)
     keep = ~ign
     assert rel_err(delta2.cpu().numpy()[keep], (ref - base.numpy())[keep]) < TOL
+
+
+@pytest.mark.parametrize("V", [4, 4096, 32768])
+@pytest.mark.parametrize("reduction", ["none", "mean"])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_fused_matches_oracle(gpu, V, reduction, accumulate):
+    N = 37
+    x, t, xd, td = _ce_case(gpu, N, V, seed=300 + V)
+    g = torch.Generator().manual_seed(10)
+    dy = torch.randn(N, generator=g) if reduction == "none" else torch.tensor([0.9])
+    base = torch.randn(N, V, generator=g)
+    delta = base.to(gpu)
+    losses, lse, reduced = torch.empty(N, device=gpu), torch.empty(N, device=gpu), torch.empty(1, device=gpu)
+    cross_entropy_fused_(losses, delta, xd, td, dy.to(gpu), -1, reduction, lse=lse, reduced=reduced,
+                         accumulate=accumulate)
+    assert rel_err(losses.cpu().numpy(), O.cross_entropy(x.numpy(), t.numpy(), -1, "none", 0)) < TOL
+    assert np.max(np.abs(lse.cpu().numpy() - O.token_lse(x.numpy()))) < TOL
+    if reduction == "mean":
+        assert abs(float(reduced) - O.cross_entropy(x.numpy(), t.numpy(), -1, "mean", 0)) < TOL
+    gref = O.cross_entropy_gradient(np.zeros((N, V)), x.numpy(), t.numpy(),
+                                    dy.numpy() if reduction == "none" else float(dy), -1, reduction, 0)
+    d = delta.cpu().numpy()
+    keep = (t != -1).numpy()
+    if accumulate:
+        ref = base.numpy() + gref
+        assert np.all(np.abs(d - ref) <= TOL * np.max(np.abs(gref)) + 2.0 ** -23 * np.abs(ref))
+    else:
+        assert rel_err(d[keep], gref[keep]) < TOL
+    assert np.array_equal(d[~keep], base.numpy()[~keep])  # ignored columns untouched
+
+
+def test_fused_rejects_what_it_cannot_hold(gpu):
+    x, t, xd, td = _ce_case(gpu, 4, 53, seed=1)
+    with pytest.raises(_lib.AttentionError, match="multiple of 4"):
+        cross_entropy_fused_(torch.empty(4, device=gpu), torch.zeros_like(xd), xd, td, 1.0, -1, "sum")
+    x = torch.zeros(2, 32772, device=gpu)
+    with pytest.raises(_lib.AttentionError, match="32768"):
+        cross_entropy_fused_(torch.empty(2, device=gpu), torch.zeros_like(x), x, torch.zeros(2, dtype=torch.int32,
+                                                                                               device=gpu), 1.0)
 
 
 def test_autograd_cross_entropy(gpu):

@@ -434,7 +434,91 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
     st = st2;
   }
 
-  // Accumulator row = key, column = head-dim index.
+  // Accumulator row = key, column = head-dim index.  The stores go through a
+  // buffer descriptor over this (batch, KV head)'s rows with the whole offset
+  // in the lane's voffset: keys at or past T fall outside the descriptor and
+  // the hardware drops them, so no store needs a branch or 64-bit address
+  // arithmetic.  (A slice of 2^31 bytes or more takes the plain loop below.)
+  const int64_t row_elems = (int64_t)a.Hkv * D;  // elements between consecutive keys
+  const int64_t slice0 = (int64_t)b * T * row_elems + (int64_t)kvh * D;
+  const int esz = a.grad_bf16 ? 2 : 4;
+  const int64_t slice_bytes = ((int64_t)(T - 1) * row_elems + D) * esz;
+  if (slice_bytes < ((int64_t)1 << 31)) {
+    const auto rk = make_rsrc(static_cast<const char*>(a.dK) + slice0 * esz, (uint32_t)slice_bytes);
+    const auto rv = make_rsrc(static_cast<const char*>(a.dV) + slice0 * esz, (uint32_t)slice_bytes);
+    // Rows 4j..4j+3 of an accumulator are four consecutive keys, and the four
+    // lanes of a quad hold four consecutive d: a 4 x 4 transpose inside each
+    // quad (two DPP butterfly stages) leaves each lane four consecutive d of
+    // one key, stored with one 8-byte (bf16) or 16-byte (fp32) store.
+    const int q = l32 & 3;
+    auto xpose = [&](float v[4]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {  // lane bit 0 <-> slot bit 0
+        const float send = (q & 1) ? v[i] : v[i + 1];
+        const float recv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+        if (q & 1) v[i] = recv;
+        else v[i + 1] = recv;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {  // lane bit 1 <-> slot bit 1
+        const float send = (q & 2) ? v[i] : v[i + 2];
+        const float recv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0x4E, 0xF, 0xF, false));
+        if (q & 2) v[i] = recv;
+        else v[i + 2] = recv;
+      }
+    };
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int d0 = 32 * db + (l32 & ~3);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float vk[4], vv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vk[i] = dk[db][4 * j + i] * a.scale;
+          vv[i] = dv[db][4 * j + i];
+        }
+        xpose(vk);  // all lanes take part in the exchange
+        xpose(vv);
+        if (d0 >= D) continue;  // whole quads (D is a multiple of 16)
+        const int kk = kw0 + acc_row(4 * j, g) + q;
+        const int voff = (int)(((int64_t)kk * row_elems + d0) * esz);
+        if (a.grad_bf16) {
+          auto pack = [](float x, float y) __attribute__((always_inline)) {
+            return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
+                   ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
+          };
+          auto unpack = [](uint32_t w, float* o) __attribute__((always_inline)) {
+            o[0] = __uint_as_float(w << 16);
+            o[1] = __uint_as_float(w & 0xffff0000u);
+          };
+          if (a.accumulate) {  // out-of-range loads read zero
+            const u32x2 ok = __builtin_amdgcn_raw_buffer_load_b64(rk, voff, 0, 0);
+            const u32x2 ov = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, 0, 0);
+            float t[4];
+            unpack(ok[0], t), unpack(ok[1], t + 2);
+            for (int i = 0; i < 4; ++i) vk[i] += t[i];
+            unpack(ov[0], t), unpack(ov[1], t + 2);
+            for (int i = 0; i < 4; ++i) vv[i] += t[i];
+          }
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vk[0], vk[1]), pack(vk[2], vk[3])}, rk, voff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vv[0], vv[1]), pack(vv[2], vv[3])}, rv, voff, 0, 0);
+        } else {
+          if (a.accumulate) {
+            const u32x4 ok = __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0);
+            const u32x4 ov = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+              vk[i] += __uint_as_float(ok[i]);
+              vv[i] += __uint_as_float(ov[i]);
+            }
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vk[0]), __float_as_uint(vk[1]), __float_as_uint(vk[2]), __float_as_uint(vk[3])}, rk, voff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vv[0]), __float_as_uint(vv[1]), __float_as_uint(vv[2]), __float_as_uint(vv[3])}, rv, voff, 0, 0);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     const int d = 32 * db + l32;

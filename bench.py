@@ -266,9 +266,18 @@ def measure_optim(dev, steps: int) -> dict:
         flops += 5 * k * (4 * lo * lo * hi + 2 * lo ** 3)
     ms = timed(lambda: [polar_express_(G, 5, w) for G, w in zip(stacks, work)], max(2, steps // 4))
     achieved = flops / (ms * 1e-3) / 1e12
-    out["polar_express"] = {"ms": round(ms, 4), "flop": flops,
+    out["polar_express"] = {"ms": round(ms, 4), "flop": flops, "compute": "fp32",
                             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
                                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4)}}
+    # scripts/train.jl passes compute_type=BFloat16 to MuonAdamW: the iteration in bf16
+    work16 = [torch.empty(polar_workspace_bytes(G, 5, torch.bfloat16), dtype=torch.uint8, device=dev) for G in stacks]
+    ms = timed(lambda: [polar_express_(G, 5, w, compute_type=torch.bfloat16) for G, w in zip(stacks, work16)],
+               max(2, steps // 4))
+    achieved = flops / (ms * 1e-3) / 1e12
+    out["polar_express_bf16"] = {"ms": round(ms, 4), "flop": flops, "compute": "bf16 (fp32 accumulation)",
+                                 "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                              "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}}
     return out
 
 

@@ -191,31 +191,39 @@ __global__ __launch_bounds__(64) void norm_finish_kernel(const double* partial, 
 }
 
 // dst (rows R, cols C, column-major) = src^T / scale (src: C rows, R cols) or
-// src / scale, per matrix (blockIdx.z), through a 32x32 LDS tile.
-template <bool kTranspose>
-__global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const float* src, float* dst,
-                                                          const float* scale) {
+// src / scale, per matrix (blockIdx.z), through a 32x32 LDS tile; the value
+// is computed in fp32 and rounded once to the destination type.
+template <typename S>
+__device__ inline float ld(const S* p) { return static_cast<float>(*p); }
+template <typename T>
+__device__ inline void st(T* p, float v) { *p = static_cast<T>(v); }
+
+template <bool kTranspose, typename S, typename T>
+__global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S* src, T* dst, const float* scale) {
   __shared__ float tile[32][33];
   const int64_t mat = (int64_t)R * C;
-  const float* s = src + blockIdx.z * mat;
-  float* d = dst + blockIdx.z * mat;
+  const S* s = src + blockIdx.z * mat;
+  T* d = dst + blockIdx.z * mat;
   const int r0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x / 32;  // 32 x 8
   if (kTranspose) {
     // d(r, c) = s(c, r): load s's columns r0.. (contiguous in c), store d's columns c0.. (contiguous in r)
     for (int j = ty; j < 32; j += 8) {
       const int r = r0 + j, c = c0 + tx;
-      if (r < R && c < C) tile[j][tx] = s[(int64_t)r * C + c];
+      if (r < R && c < C) tile[j][tx] = ld(s + (int64_t)r * C + c);
     }
     __syncthreads();
     for (int j = ty; j < 32; j += 8) {
       const int c = c0 + j, r = r0 + tx;
-      if (r < R && c < C) d[(int64_t)c * R + r] = scale ? tile[tx][j] / scale[blockIdx.z] : tile[tx][j];
+      if (r < R && c < C) st(d + (int64_t)c * R + r, scale ? tile[tx][j] / scale[blockIdx.z] : tile[tx][j]);
     }
   } else {
     for (int j = ty; j < 32; j += 8) {
       const int c = c0 + j, r = r0 + tx;
-      if (r < R && c < C) d[(int64_t)c * R + r] = scale ? s[(int64_t)c * R + r] / scale[blockIdx.z] : s[(int64_t)c * R + r];
+      if (r < R && c < C) {
+        const float v = ld(s + (int64_t)c * R + r);
+        st(d + (int64_t)c * R + r, scale ? v / scale[blockIdx.z] : v);
+      }
     }
   }
 }
@@ -226,13 +234,14 @@ struct PolarLayout {
 
 PolarLayout polar_layout(const fc_polar_desc& d) {
   const size_t lo = std::min(d.m, d.n), hi = std::max(d.m, d.n), k = d.count;
+  const size_t e = d.dtype == FC_BF16 ? 2 : 4;  // element size of the iteration buffers
   auto up = [](size_t b) { return (b + 255) / 256 * 256; };
   PolarLayout L{};
   L.X = 0;
-  L.Y = L.X + up(lo * hi * k * 4);
-  L.A = L.Y + up(lo * hi * k * 4);
-  L.B = L.A + up(lo * lo * k * 4);
-  L.scale = L.B + up(lo * lo * k * 4);
+  L.Y = L.X + up(lo * hi * k * e);
+  L.A = L.Y + up(lo * hi * k * e);
+  L.B = L.A + up(lo * lo * k * e);
+  L.scale = L.B + up(lo * lo * k * e);
   L.partial = L.scale + up(k * 4);
   L.total = L.partial + up(k * kNormParts * 8);
   return L;
@@ -258,12 +267,13 @@ rocblas_handle blas_handle(int dev) {
   return h;
 }
 
-rocblas_status gemm(rocblas_handle h, rocblas_operation ta, rocblas_operation tb, int m, int n, int k, float alpha,
-                    const float* A, int lda, int64_t sa, const float* B, int ldb, int64_t sb, float beta,
-                    const float* C, int ldc, int64_t sc, float* D, int batch) {
-  return rocblas_gemm_strided_batched_ex(h, ta, tb, m, n, k, &alpha, A, rocblas_datatype_f32_r, lda, sa, B,
-                                         rocblas_datatype_f32_r, ldb, sb, &beta, C, rocblas_datatype_f32_r, ldc, sc,
-                                         D, rocblas_datatype_f32_r, ldc, sc, batch, rocblas_datatype_f32_r,
+// D = alpha op(A) op(B) + beta C over a strided batch; operands and results
+// of type t (fp32 or bf16), fp32 accumulation and scalars.
+rocblas_status gemm(rocblas_handle h, rocblas_datatype t, rocblas_operation ta, rocblas_operation tb, int m, int n,
+                    int k, float alpha, const void* A, int lda, int64_t sa, const void* B, int ldb, int64_t sb,
+                    float beta, const void* C, int ldc, int64_t sc, void* D, int batch) {
+  return rocblas_gemm_strided_batched_ex(h, ta, tb, m, n, k, &alpha, A, t, lda, sa, B, t, ldb, sb, &beta, C, t, ldc,
+                                         sc, D, t, ldc, sc, batch, rocblas_datatype_f32_r,
                                          rocblas_gemm_algo_standard, 0, 0);
 }
 
@@ -347,7 +357,8 @@ static fc_status polar_check(const fc_polar_desc* d) {
     return failf(FC_ERR_INVALID_ARGUMENT, "polar express: sizes must be positive (m=%d n=%d count=%d steps=%d)", d->m,
                  d->n, d->count, d->steps);
   if (d->count > 65535) return failf(FC_ERR_UNSUPPORTED, "polar express: at most 65535 matrices");
-  if (d->dtype != FC_F32) return failf(FC_ERR_UNSUPPORTED, "polar express: only the FC_F32 compute type is built");
+  if (d->dtype != FC_F32 && d->dtype != FC_BF16)
+    return failf(FC_ERR_INVALID_ARGUMENT, "polar express: dtype must be FC_F32 or FC_BF16");
   return FC_OK;
 }
 
@@ -370,15 +381,15 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
     return failf(FC_ERR_WORKSPACE, "polar express: workspace must be 256-byte aligned");
   char* ws = static_cast<char*>(workspace);
-  float* X = reinterpret_cast<float*>(ws + L.X);
-  float* Y = reinterpret_cast<float*>(ws + L.Y);
-  float* A = reinterpret_cast<float*>(ws + L.A);
-  float* B = reinterpret_cast<float*>(ws + L.B);
+  char* X = ws + L.X;
+  char* Y = ws + L.Y;
+  char* A = ws + L.A;
+  char* B = ws + L.B;
   float* scale = reinterpret_cast<float*>(ws + L.scale);
   double* partial = reinterpret_cast<double*>(ws + L.partial);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int m = d->m, n = d->n, k = d->count;
-  const bool transposed = m > n;
+  const bool transposed = m > n, half = d->dtype == FC_BF16;
   const int lo = std::min(m, n), hi = std::max(m, n);
   const int64_t sx = (int64_t)lo * hi, sa = (int64_t)lo * lo;
 
@@ -386,10 +397,15 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
   if ((st = launched("polar norm")) != FC_OK) return st;
   hipLaunchKernelGGL(norm_finish_kernel, dim3(k), dim3(64), 0, s, partial, scale);
   if ((st = launched("polar norm")) != FC_OK) return st;
-  // X (lo x hi) = G / scale, or G^T / scale
-  const dim3 tiles((lo + 31) / 32, (hi + 31) / 32, k);
-  if (transposed) hipLaunchKernelGGL(copy_scaled_kernel<true>, tiles, dim3(256), 0, s, lo, hi, G, X, scale);
-  else hipLaunchKernelGGL(copy_scaled_kernel<false>, tiles, dim3(256), 0, s, lo, hi, G, X, scale);
+  // X (lo x hi) = G / scale, or G^T / scale, rounded to the compute type
+  const dim3 tiles((lo + 31) / 32, (hi + 31) / 32, k), back((hi + 31) / 32, (lo + 31) / 32, k);
+  if (half) {
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, bf16>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<bf16*>(X), scale);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, bf16>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<bf16*>(X), scale);
+  } else {
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, float>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<float*>(X), scale);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<float*>(X), scale);
+  }
   if ((st = launched("polar copy in")) != FC_OK) return st;
 
   int dev = 0;
@@ -400,22 +416,28 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
     if (h == nullptr) return failf(FC_ERR_HIP, "polar express: rocblas_create_handle failed");
     if (rocblas_set_stream(h, s) != rocblas_status_success) return failf(FC_ERR_HIP, "rocblas_set_stream failed");
     const auto N = rocblas_operation_none, T = rocblas_operation_transpose;
-    for (int t = 0; t < d->steps; ++t) {
-      const float* c = kPolar[std::min(t, 4)];
+    const rocblas_datatype t = half ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
+    for (int i = 0; i < d->steps; ++i) {
+      const float* c = kPolar[std::min(i, 4)];
       rocblas_status r;
       // A = X X^T
-      r = gemm(h, N, T, lo, lo, hi, 1.0f, X, lo, sx, X, lo, sx, 0.0f, A, lo, sa, A, k);
+      r = gemm(h, t, N, T, lo, lo, hi, 1.0f, X, lo, sx, X, lo, sx, 0.0f, A, lo, sa, A, k);
       // B = c A A + b A
-      if (r == rocblas_status_success) r = gemm(h, N, N, lo, lo, lo, c[2], A, lo, sa, A, lo, sa, c[1], A, lo, sa, B, k);
+      if (r == rocblas_status_success) r = gemm(h, t, N, N, lo, lo, lo, c[2], A, lo, sa, A, lo, sa, c[1], A, lo, sa, B, k);
       // Y = B X + a X, then X <-> Y
-      if (r == rocblas_status_success) r = gemm(h, N, N, lo, hi, lo, 1.0f, B, lo, sa, X, lo, sx, c[0], X, lo, sx, Y, k);
+      if (r == rocblas_status_success) r = gemm(h, t, N, N, lo, hi, lo, 1.0f, B, lo, sa, X, lo, sx, c[0], X, lo, sx, Y, k);
       if (r != rocblas_status_success) return failf(FC_ERR_HIP, "polar express: rocBLAS GEMM failed (%d)", (int)r);
       std::swap(X, Y);
     }
   }
-  // G = X, or X^T
-  if (transposed) hipLaunchKernelGGL(copy_scaled_kernel<true>, dim3((hi + 31) / 32, (lo + 31) / 32, k), dim3(256), 0, s, hi, lo, X, G, nullptr);
-  else hipLaunchKernelGGL(copy_scaled_kernel<false>, tiles, dim3(256), 0, s, lo, hi, X, G, nullptr);
+  // G = X, or X^T (widened to fp32)
+  if (half) {
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, bf16, float>), back, dim3(256), 0, s, hi, lo, reinterpret_cast<const bf16*>(X), G, nullptr);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, bf16, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const bf16*>(X), G, nullptr);
+  } else {
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, float>), back, dim3(256), 0, s, hi, lo, reinterpret_cast<const float*>(X), G, nullptr);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const float*>(X), G, nullptr);
+  }
   return launched("polar copy out");
 }
 

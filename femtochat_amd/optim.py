@@ -119,24 +119,30 @@ def scatter_(vector, stack, offsets, *, validate: bool = True) -> None:
                                            _stream_ptr(vector.device)))
 
 
-def _polar_desc(G, steps):
+def _polar_desc(G, steps, compute_type=torch.float32):
     if G.dim() != 3:
         raise ValueError("G must be a (k, n, m) stack (the Julia (m, n, k) array)")
+    if compute_type not in (torch.float32, torch.bfloat16):
+        raise ValueError("compute_type must be torch.float32 or torch.bfloat16")
     k, n, m = G.shape
-    return _lib.PolarDesc(m, n, k, int(steps), _lib.FC_F32)
+    return _lib.PolarDesc(m, n, k, int(steps), _lib.FC_BF16 if compute_type == torch.bfloat16 else _lib.FC_F32)
 
 
-def polar_workspace_bytes(G: torch.Tensor, steps: int = 5) -> int:
+def polar_workspace_bytes(G: torch.Tensor, steps: int = 5, compute_type=torch.float32) -> int:
     n = ctypes.c_size_t(0)
-    _lib.check(_lib.lib().fc_polar_workspace_bytes(ctypes.byref(_polar_desc(G, steps)), ctypes.byref(n)))
+    _lib.check(_lib.lib().fc_polar_workspace_bytes(ctypes.byref(_polar_desc(G, steps, compute_type)),
+                                                   ctypes.byref(n)))
     return n.value
 
 
-def polar_express_(G: torch.Tensor, steps: int = 5, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Polar Express in place on the stack G (see the module docstring for the layout)."""
+def polar_express_(G: torch.Tensor, steps: int = 5, workspace: Optional[torch.Tensor] = None,
+                   compute_type=torch.float32) -> torch.Tensor:
+    """Polar Express in place on the stack G (see the module docstring for the
+    layout); ``compute_type=torch.bfloat16`` runs the iteration in bf16 as the
+    reference's ``compute_type=BFloat16`` workspace does."""
     _f32("G", G)
-    d = _polar_desc(G, steps)
-    nbytes = polar_workspace_bytes(G, steps)
+    d = _polar_desc(G, steps, compute_type)
+    nbytes = polar_workspace_bytes(G, steps, compute_type)
     if workspace is None:
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=G.device)
     if workspace.numel() < nbytes or workspace.device != G.device:
@@ -146,5 +152,5 @@ def polar_express_(G: torch.Tensor, steps: int = 5, workspace: Optional[torch.Te
     return G
 
 
-def polar_express(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
-    return polar_express_(G.clone(), steps)
+def polar_express(G: torch.Tensor, steps: int = 5, compute_type=torch.float32) -> torch.Tensor:
+    return polar_express_(G.clone(), steps, compute_type=compute_type)

@@ -64,7 +64,9 @@ typedef struct {
   int32_t m, n;   /* rows and columns of each matrix */
   int32_t count;  /* matrices in the stack (k) */
   int32_t steps;  /* iterations (the reference's default is 5; beyond 5 the last coefficients repeat) */
-  int32_t dtype;  /* compute type of the iteration: FC_F32 */
+  int32_t dtype;  /* compute type of the iteration buffers X, A, B, Y: FC_F32, or FC_BF16 (the
+                     reference's compute_type=BFloat16, as scripts/train.jl passes it; products
+                     accumulate in fp32 and round to bf16 as they are stored) */
 } fc_polar_desc;
 
 /* Bytes of the caller-owned workspace of fc_polar_express (X, Y, A, B and

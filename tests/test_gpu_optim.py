@@ -24,6 +24,11 @@ pytestmark = pytest.mark.gpu
 
 # Polar Express: max |X - R| / max |R| against float64, and against torch fp32
 POLAR_TOL = 1e-4
+# bf16 compute type: the reference's own bf16 iteration (emulated in torch,
+# below) lies 2.5-3.3e-2 from the float64 mathematics at these sizes; this one
+# must stay within 4e-2 of float64 and no further from it than 1.5 times the
+# emulated reference, and two bf16 runs differ by both of their roundings.
+POLAR_TOL_BF16 = 4e-2
 
 
 @pytest.mark.parametrize("n,misalign", [(1_000_003, 0), (4096, 1), (7, 0)])
@@ -108,3 +113,34 @@ def test_polar_express_matches_oracle(gpu, m, n, k):
         scale = float(np.float32(1.01)) * np.sqrt(np.sum(julia[j].astype(np.float64) ** 2)) + float(np.float32(1e-6))
         s_out = np.linalg.svd(out[j].numpy().astype(np.float64), compute_uv=False)
         np.testing.assert_allclose(np.sort(s_out), np.sort(O.composed_polynomial(s_in / scale)), atol=POLAR_TOL * 4)
+
+
+def _torch_polar_bf16(G):
+    """The reference's bf16 iteration in plain torch: bf16 buffers, fp32 scalars
+    and elementwise arithmetic, products rounded to bf16."""
+    out = []
+    for g in G:
+        M = g.T
+        transposed = M.shape[0] > M.shape[1]
+        X = ((M.T if transposed else M) / (np.float32(1.01) * torch.sqrt((M * M).sum()) + np.float32(1e-6))).bfloat16()
+        for a, b, c in O.COEFFICIENTS:
+            A = (X.float() @ X.float().T.contiguous()).bfloat16()
+            B = (np.float32(b) * A.float() + np.float32(c) * (A.float() @ A.float()).bfloat16().float()).bfloat16()
+            Y = (B.float() @ X.float()).bfloat16()
+            X = (np.float32(a) * X.float() + Y.float()).bfloat16()
+        out.append((X.T if transposed else X).T.float())
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 3), (160, 48, 2), (512, 2048, 1), (2048, 512, 1)])
+def test_polar_express_bf16_compute(gpu, m, n, k):
+    g = torch.Generator().manual_seed(m * 5 + n)
+    G = torch.randn(k, n, m, generator=g)
+    out = polar_express(G.to(gpu), compute_type=torch.bfloat16).cpu()
+    julia = G.numpy().transpose(0, 2, 1)
+    ref = O.polar_express(julia).transpose(0, 2, 1)
+    e64 = rel_err(out.numpy(), ref)
+    eb = rel_err(out.numpy(), _torch_polar_bf16(G.to(gpu)).cpu().numpy())
+    e_ref_bf16 = rel_err(_torch_polar_bf16(G.to(gpu)).cpu().numpy(), ref)
+    say(f"polar bf16 {m}x{n}x{k}: vs float64 {e64:.2e}, vs torch bf16 {eb:.2e} (torch bf16 vs float64 {e_ref_bf16:.2e})")
+    assert e64 < POLAR_TOL_BF16 and e64 <= 1.5 * e_ref_bf16 and eb < 1.5 * POLAR_TOL_BF16

@@ -79,7 +79,10 @@ fc_status fc_polar_workspace_bytes(const fc_polar_desc* desc, size_t* bytes);
    then per step A = X X^T, B = b A + c A A, X = a X + B X, and G = X (or
    X^T).  The matrix products are strided-batched rocBLAS GEMMs (the
    reference's CUBLAS gemmStridedBatchedEx, ext/FemtoChatCUDAExt.jl:121-125),
-   with b A and a X folded into the products' beta terms. */
+   with b A and a X folded into the products' beta terms.  The library's
+   rocBLAS handle (one per device, created on the first call) owns rocBLAS's
+   own device workspace; everything else is in the caller's workspace.  Calls
+   from several threads are serialised while they enqueue their GEMMs. */
 fc_status fc_polar_express(const fc_polar_desc* desc, float* G, void* workspace, size_t workspace_bytes,
                            void* stream);
 

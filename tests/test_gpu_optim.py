@@ -49,6 +49,23 @@ def test_adamw_steps_are_bit_exact(gpu, n, misalign):
     assert np.array_equal(opt.m.cpu().numpy(), m) and np.array_equal(opt.v.cpu().numpy(), v)
 
 
+@pytest.mark.parametrize("t", [3, 10, 999, 12288])
+def test_adamw_bias_corrections_at_large_step_counts(gpu, t):
+    # the host forms 1 - beta^t as Julia's Float32 ^ Int does (x*x*x at t = 3,
+    # square-and-multiply in Float64 otherwise); the step must stay bit-exact
+    g = torch.Generator().manual_seed(t)
+    n = 4099
+    theta, grad = torch.randn(n, generator=g), torch.randn(n, generator=g)
+    m0, v0 = torch.randn(n, generator=g) * 0.1, torch.rand(n, generator=g) * 0.01
+    th = theta.to(gpu)
+    opt = AdamW(th, alpha=0.004, beta1=0.8, beta2=0.96, eps=1e-10, lam=0.01, t=t - 1)
+    opt.m.copy_(m0)
+    opt.v.copy_(v0)
+    opt(th, grad.to(gpu))
+    ref, m, v = O.adamw_step(theta.numpy(), grad.numpy(), m0.numpy(), v0.numpy(), t, 0.004, 0.8, 0.96, 1e-10, 0.01)
+    assert np.array_equal(th.cpu().numpy(), ref) and np.array_equal(opt.m.cpu().numpy(), m)
+
+
 def test_adam_update_is_bit_exact(gpu):
     g = torch.Generator().manual_seed(1)
     Th = torch.randn(5000, generator=g)

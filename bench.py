@@ -218,7 +218,7 @@ def measure_optim(dev, steps: int) -> dict:
     import torch
 
     from femtochat_amd import AdamW, muon_update_, polar_express_
-    from femtochat_amd.optim import polar_workspace_bytes
+    from femtochat_amd.optim import polar_express_grouped_, polar_workspace_bytes
 
     g = torch.Generator(device=dev).manual_seed(0)
     n = 1 << 26
@@ -278,6 +278,13 @@ def measure_optim(dev, steps: int) -> dict:
                                  "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                                               "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                                               "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}}
+    # the three stacks in one grouped call (concurrent on helper streams)
+    ms = timed(lambda: polar_express_grouped_(stacks, 5, work16, compute_type=torch.bfloat16), max(2, steps // 4))
+    achieved = flops / (ms * 1e-3) / 1e12
+    out["polar_express_bf16_grouped"] = {"ms": round(ms, 4), "flop": flops, "compute": "bf16, stacks concurrent",
+                                         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                                                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}}
     return out
 
 

@@ -193,6 +193,8 @@ _SIGNATURES = {
     "fc_param_scatter": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int32, _P, _P, _P, _P]),
     "fc_polar_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(PolarDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "fc_polar_express": (ctypes.c_int, [ctypes.POINTER(PolarDesc), _P, _P, ctypes.c_size_t, _P]),
+    "fc_polar_express_grouped": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(PolarDesc), ctypes.POINTER(_P),
+                                                ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_size_t), _P]),
     "fc_capabilities": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(Caps)]),
     "fc_profile_enable": (ctypes.c_int, [ctypes.c_int32]),
     "fc_profile_collect": (

@@ -269,6 +269,33 @@ rocblas_handle blas_handle(int dev) {
 
 // D = alpha op(A) op(B) + beta C over a strided batch; operands and results
 // of type t (fp32 or bf16), fp32 accumulation and scalars.
+// Helper streams for fc_polar_express_grouped: per device, kHelpers streams
+// (default priority), each with its own rocBLAS handle (so concurrent GEMMs
+// never share rocBLAS's workspace), and the fork/join events; created on
+// first use and kept until the process ends.
+constexpr int kHelpers = 4;
+struct Fork {
+  hipStream_t stream[kHelpers];
+  rocblas_handle blas[kHelpers];
+  hipEvent_t start, done[kHelpers];
+};
+Fork* g_fork[16] = {};
+
+Fork* fork_for(int dev) {
+  Fork*& f = g_fork[dev & 15];
+  if (f != nullptr) return f;
+  Fork* n = new Fork{};
+  bool ok = hipEventCreateWithFlags(&n->start, hipEventDisableTiming) == hipSuccess;
+  for (int j = 0; j < kHelpers && ok; ++j) {
+    ok = hipStreamCreateWithFlags(&n->stream[j], hipStreamNonBlocking) == hipSuccess &&
+         hipEventCreateWithFlags(&n->done[j], hipEventDisableTiming) == hipSuccess &&
+         rocblas_create_handle(&n->blas[j]) == rocblas_status_success;
+  }
+  if (!ok) return nullptr;  // (the partial objects are left to the process end)
+  f = n;
+  return f;
+}
+
 rocblas_status gemm(rocblas_handle h, rocblas_datatype t, rocblas_operation ta, rocblas_operation tb, int m, int n,
                     int k, float alpha, const void* A, int lda, int64_t sa, const void* B, int ldb, int64_t sb,
                     float beta, const void* C, int ldc, int64_t sc, void* D, int batch) {
@@ -371,7 +398,10 @@ fc_status fc_polar_workspace_bytes(const fc_polar_desc* d, size_t* bytes) {
   return FC_OK;
 }
 
-fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, void* stream) {
+// Polar Express of one stack on stream s with the rocBLAS handle h (held by
+// the caller under g_blas_mutex).
+static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, hipStream_t s,
+                           rocblas_handle h) {
   fc_status st = polar_check(d);
   if (st != FC_OK) return st;
   if (G == nullptr) return failf(FC_ERR_INVALID_ARGUMENT, "polar express: G is null");
@@ -387,7 +417,6 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
   char* B = ws + L.B;
   float* scale = reinterpret_cast<float*>(ws + L.scale);
   double* partial = reinterpret_cast<double*>(ws + L.partial);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int m = d->m, n = d->n, k = d->count;
   const bool transposed = m > n, half = d->dtype == FC_BF16;
   const int lo = std::min(m, n), hi = std::max(m, n);
@@ -408,12 +437,7 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
   }
   if ((st = launched("polar copy in")) != FC_OK) return st;
 
-  int dev = 0;
-  hipGetDevice(&dev);
   {
-    std::lock_guard<std::mutex> lock(g_blas_mutex);
-    rocblas_handle h = blas_handle(dev);
-    if (h == nullptr) return failf(FC_ERR_HIP, "polar express: rocblas_create_handle failed");
     if (rocblas_set_stream(h, s) != rocblas_status_success) return failf(FC_ERR_HIP, "rocblas_set_stream failed");
     const auto N = rocblas_operation_none, T = rocblas_operation_transpose;
     const rocblas_datatype t = half ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
@@ -439,6 +463,48 @@ fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, si
     else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const float*>(X), G, nullptr);
   }
   return launched("polar copy out");
+}
+
+fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, void* stream) {
+  int dev = 0;
+  hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lock(g_blas_mutex);
+  rocblas_handle h = blas_handle(dev);
+  if (h == nullptr) return failf(FC_ERR_HIP, "polar express: rocblas_create_handle failed");
+  return polar_run(d, G, workspace, workspace_bytes, static_cast<hipStream_t>(stream), h);
+}
+
+fc_status fc_polar_express_grouped(int32_t count, const fc_polar_desc* descs, float* const* G, void* const* workspaces,
+                                   const size_t* workspace_bytes, void* stream) {
+  if (count <= 0 || descs == nullptr || G == nullptr || workspaces == nullptr || workspace_bytes == nullptr)
+    return failf(FC_ERR_INVALID_ARGUMENT, "polar express grouped: count must be positive and the arrays non-null");
+  for (int i = 0; i < count; ++i) {
+    const fc_status st = polar_check(&descs[i]);
+    if (st != FC_OK) return st;
+  }
+  int dev = 0;
+  hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lock(g_blas_mutex);
+  Fork* f = fork_for(dev);
+  if (f == nullptr) return failf(FC_ERR_HIP, "polar express grouped: helper streams could not be created");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // fork: every helper stream waits for the caller's stream
+  if (hipEventRecord(f->start, s) != hipSuccess) return failf(FC_ERR_HIP, "hipEventRecord failed");
+  const int used = std::min<int>(count, kHelpers);
+  for (int j = 0; j < used; ++j)
+    if (hipStreamWaitEvent(f->stream[j], f->start, 0) != hipSuccess) return failf(FC_ERR_HIP, "hipStreamWaitEvent failed");
+  for (int i = 0; i < count; ++i) {
+    const int j = i % kHelpers;
+    const fc_status st = polar_run(&descs[i], G[i], workspaces[i], workspace_bytes[i], f->stream[j], f->blas[j]);
+    if (st != FC_OK) return st;
+  }
+  // join: the caller's stream waits for every helper stream
+  for (int j = 0; j < used; ++j) {
+    if (hipEventRecord(f->done[j], f->stream[j]) != hipSuccess || hipStreamWaitEvent(s, f->done[j], 0) != hipSuccess)
+      return failf(FC_ERR_HIP, "polar express grouped: join failed");
+  }
+  clear_error();
+  return FC_OK;
 }
 
 }  // extern "C"

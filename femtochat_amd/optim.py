@@ -27,7 +27,7 @@ from . import _lib
 from .kernels import _ptr, _stream_ptr
 
 __all__ = ["AdamW", "adamw_step_", "adam_update_", "muon_update_", "gather_", "scatter_", "polar_express_",
-           "polar_express", "polar_workspace_bytes"]
+           "polar_express_grouped_", "polar_express", "polar_workspace_bytes"]
 
 
 def _f32(name, t, device=None):
@@ -150,6 +150,30 @@ def polar_express_(G: torch.Tensor, steps: int = 5, workspace: Optional[torch.Te
     _lib.check(_lib.lib().fc_polar_express(ctypes.byref(d), _ptr(G), _ptr(workspace), workspace.numel(),
                                            _stream_ptr(G.device)))
     return G
+
+
+def polar_express_grouped_(stacks, steps: int = 5, workspaces=None, compute_type=torch.float32):
+    """Polar Express in place on several stacks at once (the reference's Muon
+    groups, one per matrix shape), run concurrently on helper streams forked
+    from and joined to the current stream."""
+    stacks = list(stacks)
+    if not stacks:
+        return stacks
+    dev = stacks[0].device
+    for G in stacks:
+        _f32("G", G, dev)
+    descs = (_lib.PolarDesc * len(stacks))(*[_polar_desc(G, steps, compute_type) for G in stacks])
+    sizes = [polar_workspace_bytes(G, steps, compute_type) for G in stacks]
+    if workspaces is None:
+        workspaces = [torch.empty(n, dtype=torch.uint8, device=dev) for n in sizes]
+    for w, n in zip(workspaces, sizes):
+        if w.numel() < n or w.device != dev:
+            raise ValueError("each workspace must hold polar_workspace_bytes(G) bytes on G's device")
+    gp = (ctypes.c_void_p * len(stacks))(*[G.data_ptr() for G in stacks])
+    wp = (ctypes.c_void_p * len(stacks))(*[w.data_ptr() for w in workspaces])
+    wb = (ctypes.c_size_t * len(stacks))(*[w.numel() for w in workspaces])
+    _lib.check(_lib.lib().fc_polar_express_grouped(len(stacks), descs, gp, wp, wb, _stream_ptr(dev)))
+    return stacks
 
 
 def polar_express(G: torch.Tensor, steps: int = 5, compute_type=torch.float32) -> torch.Tensor:

@@ -86,6 +86,16 @@ fc_status fc_polar_workspace_bytes(const fc_polar_desc* desc, size_t* bytes);
 fc_status fc_polar_express(const fc_polar_desc* desc, float* G, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Polar Express of several stacks at once (the reference's Muon groups,
+   src/optim.jl:278-309, one per matrix shape), each as fc_polar_express with
+   its own workspace.  The stacks run concurrently on four helper streams
+   forked from and joined back to the caller's stream with events, so the
+   small batched GEMMs of different stacks share the GPU; the helper streams,
+   their rocBLAS handles and the events are created on the first call per
+   device and kept until the process ends. */
+fc_status fc_polar_express_grouped(int32_t count, const fc_polar_desc* descs, float* const* G,
+                                   void* const* workspaces, const size_t* workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

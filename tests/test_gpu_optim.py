@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from femtochat_amd import AdamW, adam_update_, gather_, muon_update_, polar_express, scatter_
+from femtochat_amd.optim import polar_express_grouped_
 from oracle import optim as O
 
 from tests.helpers import rel_err, say
@@ -161,3 +162,18 @@ def test_polar_express_bf16_compute(gpu, m, n, k):
     e_ref_bf16 = rel_err(_torch_polar_bf16(G.to(gpu)).cpu().numpy(), ref)
     say(f"polar bf16 {m}x{n}x{k}: vs float64 {e64:.2e}, vs torch bf16 {eb:.2e} (torch bf16 vs float64 {e_ref_bf16:.2e})")
     assert e64 < POLAR_TOL_BF16 and e64 <= 1.5 * e_ref_bf16 and eb < 1.5 * POLAR_TOL_BF16
+
+
+@pytest.mark.parametrize("compute_type", [torch.float32, torch.bfloat16])
+def test_grouped_equals_separate_calls(gpu, compute_type):
+    # the stacks run concurrently on helper streams, each with the same GEMMs as
+    # a call of its own: the results are identical
+    g = torch.Generator().manual_seed(17)
+    shapes = [(64, 64, 5), (48, 160, 3), (160, 48, 2), (96, 96, 1), (32, 80, 4)]  # five stacks, four helpers
+    stacks = [torch.randn(k, n, m, generator=g).to(gpu) for m, n, k in shapes]
+    separate = [polar_express(G, compute_type=compute_type) for G in stacks]
+    grouped = [G.clone() for G in stacks]
+    polar_express_grouped_(grouped, compute_type=compute_type)
+    torch.cuda.synchronize()
+    for a, b in zip(separate, grouped):
+        assert torch.equal(a, b)

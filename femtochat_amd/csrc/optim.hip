@@ -15,6 +15,7 @@
 #include "../../include/femtochat_optim.h"
 #include "attn_launch.hpp"
 #include "attn_device.hpp"
+#include "attn_fast.hpp"
 
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
@@ -228,6 +229,272 @@ __global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S*
   }
 }
 
+// ---- bf16 batched GEMM of the Polar Express iteration ------------------------------
+// D(i, j) = alpha sum_k P(i, k) Q(k, j) + beta C(i, j), per matrix of a strided
+// batch, bf16 operands, fp32 accumulation, one rounding to bf16 at the store.
+//   kTr:  P(i, k) at P[k ldp + i], Q(k, j) at Q[k ldq + j]  (contiguous in i, j)
+//   else: P(i, k) at P[i ldp + k], Q(k, j) at Q[j ldq + k]  (contiguous in k)
+//   C, D  column-major M x N (leading dimension M)
+// A workgroup of four waves computes a 128 x 128 tile of D, each wave 64 x 64
+// as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16.  The k loop runs in steps of
+// 64 through two LDS stages filled by direct global->LDS loads (the next
+// step's loads are in flight while the current step's products run; one
+// barrier per step):
+//   * kTr: k-major tiles (64 rows of k, 128 values of i or j, 256 B per row,
+//     the 16-byte units of row r XOR-swizzled by 4(r mod 4) + (r/4 mod 4)),
+//     read with ds_read_b64_tr_b16, four k of one column per 8-byte read;
+//   * otherwise i- and j-major tiles (128 rows, 64 k, 128 B per row, units
+//     swizzled by (r/2) mod 8), one 16-byte read per fragment (the transposed
+//     reads take about twice as long for the same bytes).
+// Both reads are free of bank conflicts and give lane l (g = l/32) the column
+// l mod 32 and k = 8g + e, e < 8, so P and Q fragments pair in the MFMA.
+// M, N multiples of 128, K a multiple of 64, every operand under 2^31 bytes
+// (checked by the caller): all tiles are whole and every offset is 32-bit.
+struct PolarGemm {
+  const bf16* P;
+  const bf16* Q;
+  const bf16* C;
+  bf16* D;
+  int64_t sp, sq, sd;  // batch strides (elements); C has D's
+  int ldp, ldq;
+  int M, N, K;
+  float alpha, beta;
+};
+
+constexpr int kGemmTile = 128, kGemmK = 64;
+// epilogue quadrant: 64 columns of 64 fp32, padded to 272 bytes (conflict-free
+// 16-byte writes by column and reads by row group)
+constexpr int kQuadPitch = 272, kQuadBytes = 64 * kQuadPitch;
+
+template <int kUPR>
+__device__ constexpr int gemm_swz(int r) {
+  return kUPR == 16 ? (4 * (r & 3) + ((r >> 2) & 3)) : ((r >> 1) & 7);
+}
+
+// Per-lane global byte offsets of one wave's share of a tile's DMA: kRows
+// rows of kUPR 16-byte units, 1 KB blocks, block b filled by wave b mod 4;
+// lane l of block b writes physical unit 64 b + l.
+template <int kUPR>
+struct GemmDma {
+  static constexpr int kRows = 1024 / kUPR;  // 16 KB tiles
+  static constexpr int kPer = kRows * kUPR / 64 / kWaves;
+  int goff[kPer];
+  __device__ inline void init(int wave, int lane, int pitch_bytes) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int unit = 64 * (wave + kWaves * j) + lane;
+      const int row = unit / kUPR, pu = unit % kUPR;
+      goff[j] = row * pitch_bytes + 16 * (pu ^ gemm_swz<kUPR>(row));
+    }
+  }
+  __device__ inline void issue(u32x4s words, int tile_off, uint32_t lds, int wave) const {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      dma_load16(words, goff[j] + tile_off, __builtin_amdgcn_readfirstlane(lds + 1024 * (wave + kWaves * j)));
+  }
+};
+
+// Waits until at most N of this wave's global loads (LDS-DMA included) are
+// outstanding (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and
+// lgkmcnt left at their maxima, i.e. not waited for).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <bool kTr, int kStages>
+__global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(PolarGemm a) {
+  // kStages stages of [P, Q] tiles; after the k loop, each wave's 64 x 64
+  // fp32 quadrant (columns of kQuadPitch bytes)
+  constexpr int kLds = 32768 * kStages > 4 * kQuadBytes ? 32768 * kStages : 4 * kQuadBytes;
+  __shared__ __attribute__((aligned(1024))) char lds[kLds];
+  auto tile = [&](int stage, int which) __attribute__((always_inline)) { return lds + 32768 * stage + 16384 * which; };
+  const int tm = a.M / kGemmTile, tiles = tm * (a.N / kGemmTile);
+  // XCD-aware order: workgroup w runs on XCD w mod 8, so the eight XCDs take
+  // contiguous runs of tiles (whole matrices, sharing operands in their L2)
+  int w = blockIdx.x;
+  if ((gridDim.x & 7) == 0) w = (w & 7) * (gridDim.x >> 3) + (w >> 3);
+  const int b = w / tiles, t = w - b * tiles;
+  const int i0 = (t % tm) * kGemmTile, j0 = (t / tm) * kGemmTile;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wi = wave & 1, wj = wave >> 1, l32 = lane & 31, g = lane >> 5;
+
+  const u32x4s pw = buffer_words(a.P + b * a.sp, (uint32_t)((int64_t)(kTr ? a.K : a.M) * a.ldp * 2));
+  const u32x4s qw = buffer_words(a.Q + b * a.sq, (uint32_t)((int64_t)(kTr ? a.K : a.N) * a.ldq * 2));
+  using Dma = GemmDma<kTr ? 16 : 8>;
+  Dma pdma, qdma;
+  pdma.init(wave, lane, 2 * a.ldp);
+  qdma.init(wave, lane, 2 * a.ldq);
+  // tile origin of k step s: rows 64s, columns i0 (P) or j0 (Q) when kTr,
+  // else rows i0 or j0, columns 64s
+  auto issue = [&](int s, int stage) __attribute__((always_inline)) {
+    pdma.issue(pw, kTr ? 2 * (kGemmK * s * a.ldp + i0) : 2 * (i0 * a.ldp + kGemmK * s), lds_addr(tile(stage, 0)), wave);
+    qdma.issue(qw, kTr ? 2 * (kGemmK * s * a.ldq + j0) : 2 * (j0 * a.ldq + kGemmK * s), lds_addr(tile(stage, 1)), wave);
+  };
+
+  // fragment offsets: k-major tiles (rows 8g + 4e + a, a = (lane mod 16)/4,
+  // column 16 ((lane/16) mod 2) + 4 (lane mod 4), +64 B per 32-column block)
+  int tr[2];
+  {
+    const int s = lane & 15, ar = s >> 2, cc = s & 3, u = 2 * ((lane >> 4) & 1) + (cc >> 1);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 8 * g + 4 * e + ar;
+      tr[e] = 256 * r + 16 * (u ^ gemm_swz<16>(r)) + 8 * (cc & 1);
+    }
+  }
+  // i- or j-major tiles: row 64 wi + 32 x + l32 (P) or 64 wj + 32 y + l32 (Q),
+  // unit 2c + g (chunk c is ^ 32c)
+  const int nat = l32 * 128 + 16 * (g ^ gemm_swz<8>(l32));
+  const int natp = nat + 64 * 128 * wi, natq = nat + 64 * 128 * wj;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.0f;
+
+  // The output leaves through LDS: lane l of a wave owns, in pass t < 8, column
+  // 8t + l/8 of its quadrant, rows 8 (l mod 8) .. +7 (16 bytes of bf16), so
+  // eight lanes write one whole 128-byte column segment.  C is loaded in the
+  // same layout before the k loop (its loads complete under the first wait).
+  const int64_t dbytes = (int64_t)a.M * a.N * 2;
+  const auto rd = make_rsrc(a.D + b * a.sd, (uint32_t)dbytes);
+  const bool has_c = a.beta != 0.0f;  // without C the loads read zero records: no memory access
+  const auto rc = make_rsrc(has_c ? a.C + b * a.sd : a.D, has_c ? (uint32_t)dbytes : 0u);
+  const int orow = 64 * wi + 8 * (lane & 7), ocol = 64 * wj + (lane >> 3);
+  auto out_off = [&](int t) __attribute__((always_inline)) { return 2 * ((j0 + ocol + 8 * t) * a.M + i0 + orow); };
+  u32x4 cw[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) cw[t] = __builtin_amdgcn_raw_buffer_load_b128(rc, out_off(t), 0, 0);
+
+  // k steps s .. s + kStages - 2 are in flight while step s is multiplied
+  // (each wave issues kDmaPer loads per step); a step's stage is refilled
+  // after the barrier that follows every wave's last read of it
+  constexpr int kDmaPer = 2 * Dma::kPer;
+  const int steps = a.K / kGemmK;
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < steps) issue(s, s);
+  for (int s = 0; s < steps; ++s) {
+    const int stage = s % kStages;
+    if (s + kStages - 2 < steps) wait_vmcnt<kDmaPer * (kStages - 2)>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (s + kStages - 1 < steps) issue(s + kStages - 1, (s + kStages - 1) % kStages);
+    const char* pt = tile(stage, 0);
+    const char* qt = tile(stage, 1);
+    // fragments of chunk c + 1 are read while chunk c's products run
+    bf16x8 pf[2][2], qf[2][2];
+    auto read = [&](int c, bf16x8* p, bf16x8* q) __attribute__((always_inline)) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        if (kTr) {
+          const int blk = 128 * wi + 64 * x;
+          p[x] = lds_tr_frag(pt, (tr[0] + 4096 * c) ^ blk, (tr[1] + 4096 * c) ^ blk);
+        } else {
+          p[x] = as_bf16x8(lds_load16(pt, (natp + 4096 * x) ^ (32 * c)));
+        }
+      }
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        if (kTr) {
+          const int blk = 128 * wj + 64 * y;
+          q[y] = lds_tr_frag(qt, (tr[0] + 4096 * c) ^ blk, (tr[1] + 4096 * c) ^ blk);
+        } else {
+          q[y] = as_bf16x8(lds_load16(qt, (natq + 4096 * y) ^ (32 * c)));
+        }
+      }
+    };
+    read(0, pf[0], qf[0]);
+#pragma unroll
+    for (int c = 0; c < kGemmK / 16; ++c) {
+      if (c + 1 < kGemmK / 16) read(c + 1, pf[(c + 1) & 1], qf[(c + 1) & 1]);
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf[c & 1][x], qf[c & 1][y], acc[x][y], 0, 0, 0);
+    }
+    // keep that order through scheduling: LDS reads of chunk c + 1 ahead of
+    // the products of chunk c (masks: 0x100 LDS read, 0x008 MFMA)
+    constexpr int kReads = kTr ? 8 : 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+#pragma unroll
+    for (int c = 0; c < kGemmK / 16 - 1; ++c) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  }
+  __syncthreads();  // every wave's last reads of the stages precede the quadrant writes
+
+  // accumulators -> the wave's quadrant in LDS: lane l holds column l32 of
+  // each block and rows 8q + 4g + 0..3 (q < 4), one 16-byte write each
+  char* quad = lds + wave * kQuadBytes;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = a.alpha * acc[x][y][4 * q + e];
+        *reinterpret_cast<f32x4*>(quad + (32 * y + l32) * kQuadPitch + 4 * (32 * x + 8 * q + 4 * g)) = v;
+      }
+  __syncthreads();
+  auto pack = [](float x, float y) __attribute__((always_inline)) {
+    return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
+           ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
+  };
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const char* src = quad + (8 * t + (lane >> 3)) * kQuadPitch + 32 * (lane & 7);
+    const f32x4 lo4 = *reinterpret_cast<const f32x4*>(src), hi4 = *reinterpret_cast<const f32x4*>(src + 16);
+    float v[8] = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+    if (has_c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] += a.beta * __uint_as_float(cw[t][e] << 16);
+        v[2 * e + 1] += a.beta * __uint_as_float(cw[t][e] & 0xffff0000u);
+      }
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{pack(v[0], v[1]), pack(v[2], v[3]), pack(v[4], v[5]), pack(v[6], v[7])},
+                                           rd, out_off(t), 0, 0);
+  }
+}
+
+// True when the Polar Express products of these sizes fit polar_gemm_kernel.
+bool polar_gemm_fits(int lo, int hi) {
+  return lo % kGemmTile == 0 && hi % kGemmTile == 0 && (int64_t)lo * hi * 2 < ((int64_t)1 << 31);
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cus[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  int& c = cus[dev & 15];
+  if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) c = 256;
+  return c;
+}
+
+// Two stages (two workgroups per CU) when the grid fills the GPU twice over,
+// otherwise three (one workgroup per CU, two k steps in flight).
+void polar_gemm(bool tr, const PolarGemm& a, int batch, hipStream_t s, int cus) {
+  const int64_t grid = (int64_t)(a.M / kGemmTile) * (a.N / kGemmTile) * batch;
+  const bool deep = grid < 2 * (int64_t)cus;
+  const dim3 g((unsigned)grid), b(256);
+  if (tr && deep) hipLaunchKernelGGL((polar_gemm_kernel<true, 3>), g, b, 0, s, a);
+  else if (tr) hipLaunchKernelGGL((polar_gemm_kernel<true, 2>), g, b, 0, s, a);
+  else if (deep) hipLaunchKernelGGL((polar_gemm_kernel<false, 3>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((polar_gemm_kernel<false, 2>), g, b, 0, s, a);
+}
+
 struct PolarLayout {
   size_t X, Y, A, B, scale, partial, total;
 };
@@ -437,7 +704,27 @@ static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, si
   }
   if ((st = launched("polar copy in")) != FC_OK) return st;
 
-  {
+  if (half && polar_gemm_fits(lo, hi)) {
+    const bf16* none = nullptr;
+    const int cus = cu_count();
+    for (int i = 0; i < d->steps; ++i) {
+      const float* c = kPolar[std::min(i, 4)];
+      bf16* x = reinterpret_cast<bf16*>(X);
+      bf16* y = reinterpret_cast<bf16*>(Y);
+      bf16* a = reinterpret_cast<bf16*>(A);
+      bf16* b = reinterpret_cast<bf16*>(B);
+      // A = X X^T: P(i, p) = X(i, p), Q(p, j) = X(j, p), both contiguous in i, j
+      polar_gemm(true, PolarGemm{x, x, none, a, sx, sx, sa, lo, lo, lo, lo, hi, 1.0f, 0.0f}, k, s, cus);
+      // B = c A A + b A: Q(q, j) = A(q, j), contiguous in q; A is symmetric
+      // (X X^T), so P(i, q) is read as A(q, i), also contiguous in q
+      polar_gemm(false, PolarGemm{a, a, a, b, sa, sa, sa, lo, lo, lo, lo, lo, c[2], c[1]}, k, s, cus);
+      // Y = B X + a X: Q(q, p) = X(q, p), contiguous in q; P(i, q) read as
+      // B(q, i) (B = c A A + b A is symmetric)
+      polar_gemm(false, PolarGemm{b, x, x, y, sa, sx, sx, lo, lo, lo, hi, lo, 1.0f, c[0]}, k, s, cus);
+      std::swap(X, Y);
+    }
+    if ((st = launched("polar express GEMM")) != FC_OK) return st;
+  } else {
     if (rocblas_set_stream(h, s) != rocblas_status_success) return failf(FC_ERR_HIP, "rocblas_set_stream failed");
     const auto N = rocblas_operation_none, T = rocblas_operation_transpose;
     const rocblas_datatype t = half ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;

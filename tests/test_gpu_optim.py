@@ -150,7 +150,9 @@ def _torch_polar_bf16(G):
     return torch.stack(out)
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 64, 3), (160, 48, 2), (512, 2048, 1), (2048, 512, 1)])
+# sizes that are multiples of 128 run the library's own MFMA GEMM, the others rocBLAS
+@pytest.mark.parametrize("m,n,k", [(64, 64, 3), (160, 48, 2), (128, 128, 3), (256, 384, 2), (384, 256, 2),
+                                   (512, 512, 4), (512, 2048, 1), (2048, 512, 1)])
 def test_polar_express_bf16_compute(gpu, m, n, k):
     g = torch.Generator().manual_seed(m * 5 + n)
     G = torch.randn(k, n, m, generator=g)
@@ -169,7 +171,8 @@ def test_grouped_equals_separate_calls(gpu, compute_type):
     # the stacks run concurrently on helper streams, each with the same GEMMs as
     # a call of its own: the results are identical
     g = torch.Generator().manual_seed(17)
-    shapes = [(64, 64, 5), (48, 160, 3), (160, 48, 2), (96, 96, 1), (32, 80, 4)]  # five stacks, four helpers
+    # six stacks on four helpers; the last two run the library's own GEMM in bf16
+    shapes = [(64, 64, 5), (48, 160, 3), (160, 48, 2), (96, 96, 1), (128, 256, 2), (384, 128, 3)]
     stacks = [torch.randn(k, n, m, generator=g).to(gpu) for m, n, k in shapes]
     separate = [polar_express(G, compute_type=compute_type) for G in stacks]
     grouped = [G.clone() for G in stacks]

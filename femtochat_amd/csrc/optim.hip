@@ -259,6 +259,10 @@ struct PolarGemm {
   int ldp, ldq;
   int M, N, K;
   float alpha, beta;
+  // gmode 1: instead of D, G[j M + i] = D(i, j) widened to fp32; gmode 2:
+  // G[i N + j] = D(i, j) (the transpose), both per matrix of M N floats
+  float* G = nullptr;
+  int gmode = 0;
 };
 
 constexpr int kGemmTile = 128, kGemmK = 64;
@@ -365,6 +369,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
   const auto rd = make_rsrc(a.D + b * a.sd, (uint32_t)dbytes);
   const bool has_c = a.beta != 0.0f;  // without C the loads read zero records: no memory access
   const auto rc = make_rsrc(has_c ? a.C + b * a.sd : a.D, has_c ? (uint32_t)dbytes : 0u);
+  const auto rg = make_rsrc(a.gmode != 0 ? static_cast<const void*>(a.G + b * (int64_t)a.M * a.N) : a.D, a.gmode != 0 ? (uint32_t)(2 * dbytes) : 0u);
   const int orow = 64 * wi + 8 * (lane & 7), ocol = 64 * wj + (lane >> 3);
   auto out_off = [&](int t) __attribute__((always_inline)) { return 2 * ((j0 + ocol + 8 * t) * a.M + i0 + orow); };
   u32x4 cw[8];
@@ -463,14 +468,46 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
         v[2 * e + 1] += a.beta * __uint_as_float(cw[t][e] & 0xffff0000u);
       }
     }
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{pack(v[0], v[1]), pack(v[2], v[3]), pack(v[4], v[5]), pack(v[6], v[7])},
-                                           rd, out_off(t), 0, 0);
+    if (a.gmode == 0) {
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{pack(v[0], v[1]), pack(v[2], v[3]), pack(v[4], v[5]), pack(v[6], v[7])},
+                                             rd, out_off(t), 0, 0);
+      continue;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(static_cast<bf16>(v[e]));  // the bf16 iterate, widened
+    if (a.gmode == 1) {
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                             rg, 2 * out_off(t), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])},
+                                             rg, 2 * out_off(t) + 16, 0, 0);
+    } else {  // back into the quadrant, for the transposed pass
+      *reinterpret_cast<f32x4*>(const_cast<char*>(src)) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(const_cast<char*>(src) + 16) = f32x4{v[4], v[5], v[6], v[7]};
+    }
+  }
+  if (a.gmode == 2) {
+    // lane l, pass t: quadrant row 8t + l/8, columns 8 (l mod 8) .. +7, i.e.
+    // 32 contiguous bytes of a row of G^T (eight lanes: one 256-byte row segment)
+    __syncthreads();
+    const int c0 = 8 * (lane & 7);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int r = 8 * t + (lane >> 3);
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = *reinterpret_cast<const float*>(quad + (c0 + e) * kQuadPitch + 4 * r);
+      const int goff = 4 * ((i0 + 64 * wi + r) * a.N + j0 + 64 * wj + c0);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                             rg, goff, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])},
+                                             rg, goff + 16, 0, 0);
+    }
   }
 }
 
 // True when the Polar Express products of these sizes fit polar_gemm_kernel.
 bool polar_gemm_fits(int lo, int hi) {
-  return lo % kGemmTile == 0 && hi % kGemmTile == 0 && (int64_t)lo * hi * 2 < ((int64_t)1 << 31);
+  return lo % kGemmTile == 0 && hi % kGemmTile == 0 && (int64_t)lo * hi * 4 < ((int64_t)1 << 31);
 }
 
 // Compute units of the current device (cached per device).
@@ -720,10 +757,15 @@ static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, si
       polar_gemm(false, PolarGemm{a, a, a, b, sa, sa, sa, lo, lo, lo, lo, lo, c[2], c[1]}, k, s, cus);
       // Y = B X + a X: Q(q, p) = X(q, p), contiguous in q; P(i, q) read as
       // B(q, i) (B = c A A + b A is symmetric)
-      polar_gemm(false, PolarGemm{b, x, x, y, sa, sx, sx, lo, lo, lo, hi, lo, 1.0f, c[0]}, k, s, cus);
+      // (the last step writes G itself: the bf16 iterate widened to fp32, as
+      // G = X or X^T)
+      const bool last = i + 1 == d->steps;
+      polar_gemm(false, PolarGemm{b, x, x, y, sa, sx, sx, lo, lo, lo, hi, lo, 1.0f, c[0], G, last ? (transposed ? 2 : 1) : 0},
+                 k, s, cus);
       std::swap(X, Y);
     }
     if ((st = launched("polar express GEMM")) != FC_OK) return st;
+    if (d->steps > 0) return FC_OK;
   } else {
     if (rocblas_set_stream(h, s) != rocblas_status_success) return failf(FC_ERR_HIP, "rocblas_set_stream failed");
     const auto N = rocblas_operation_none, T = rocblas_operation_transpose;

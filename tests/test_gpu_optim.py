@@ -166,6 +166,40 @@ def test_polar_express_bf16_compute(gpu, m, n, k):
     assert e64 < POLAR_TOL_BF16 and e64 <= 1.5 * e_ref_bf16 and eb < 1.5 * POLAR_TOL_BF16
 
 
+def _torch_polar_bf16_steps(G, steps):
+    out = []
+    for g in G:
+        M = g.T
+        transposed = M.shape[0] > M.shape[1]
+        X = ((M.T if transposed else M) / (np.float32(1.01) * torch.sqrt((M * M).sum()) + np.float32(1e-6))).bfloat16()
+        for t in range(steps):
+            a, b, c = O.COEFFICIENTS[min(t, len(O.COEFFICIENTS) - 1)]
+            A = (X.float() @ X.float().T.contiguous()).bfloat16()
+            B = (np.float32(b) * A.float() + np.float32(c) * (A.float() @ A.float()).bfloat16().float()).bfloat16()
+            X = (np.float32(a) * X.float() + (B.float() @ X.float()).bfloat16().float()).bfloat16()
+        out.append((X.T if transposed else X).T.float())
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("steps", [0, 1, 2, 7])
+@pytest.mark.parametrize("m,n", [(256, 384), (384, 256)])
+def test_polar_express_bf16_step_counts(gpu, m, n, steps):
+    # the library's GEMM path writes G from the last step's product (as G or
+    # its transpose); with no steps G is the normalised input rounded to bf16
+    g = torch.Generator().manual_seed(steps * 31 + m)
+    G = torch.randn(2, n, m, generator=g)
+    out = polar_express(G.to(gpu), steps, compute_type=torch.bfloat16).cpu()
+    julia = G.numpy().transpose(0, 2, 1)
+    ref = O.polar_express(julia, steps).transpose(0, 2, 1)
+    emu = _torch_polar_bf16_steps(G.to(gpu), steps).cpu().numpy()
+    e64, eb = rel_err(out.numpy(), ref), rel_err(out.numpy(), emu)
+    say(f"polar bf16 {m}x{n} steps={steps}: vs float64 {e64:.2e}, vs torch bf16 {eb:.2e}")
+    if steps == 0:  # the normalised input, rounded once to bf16 (within one bf16 unit of float64)
+        assert np.all(np.abs(out.numpy() - ref) <= 2.0 ** -8 * np.abs(ref))
+    else:
+        assert e64 < POLAR_TOL_BF16 and eb < 1.5 * POLAR_TOL_BF16
+
+
 @pytest.mark.parametrize("compute_type", [torch.float32, torch.bfloat16])
 def test_grouped_equals_separate_calls(gpu, compute_type):
     # the stacks run concurrently on helper streams, each with the same GEMMs as

@@ -211,10 +211,11 @@ def measure_optim(dev, steps: int) -> dict:
     defaults: n_embed 512, 8 layers, vocabulary 2^15): one AdamW step over
     2^26 fp32 parameters (the embedding, value-embedding and head matrices'
     scale), Muon's final write over the block matrices, and Polar Express
-    (5 steps, fp32) over their stacks: 32 of 512x512, 8 of 512x2048 and 8 of
-    2048x512.  AdamW and the write are HBM-bound (bytes per unit time against
-    8 TB/s); Polar Express is GEMMs (rocBLAS): FLOP per unit time against the
-    fp32 MFMA peak.  Not part of the headline value."""
+    (5 steps, fp32 and bf16) over their stacks: 32 of 512x512, 8 of 512x2048
+    and 8 of 2048x512.  AdamW and the write are HBM-bound (bytes per unit time
+    against 8 TB/s); Polar Express is batched products (rocBLAS in fp32, the
+    library's MFMA kernel in bf16): FLOP per unit time against the fp32 or
+    bf16 MFMA peak.  Not part of the headline value."""
     import torch
 
     from femtochat_amd import AdamW, muon_update_, polar_express_

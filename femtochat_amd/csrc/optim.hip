@@ -10,8 +10,10 @@
 // Polar Express (src/optim.jl:115-149) normalises each matrix by its
 // Frobenius norm (a two-stage float64 reduction), copies it into the iteration
 // buffer (transposed through LDS when m > n, so the Gram matrix is the
-// smaller one), runs three strided-batched rocBLAS GEMMs per step with the
-// elementwise terms folded into their beta, and copies the result back.
+// smaller one) and runs three batched products per step with the elementwise
+// terms folded into their beta: in bf16, for sizes that are multiples of 128,
+// the MFMA kernel below (whose last product writes the result), otherwise
+// strided-batched rocBLAS GEMMs followed by a copy back.
 #include "../../include/femtochat_optim.h"
 #include "attn_launch.hpp"
 #include "attn_device.hpp"

@@ -77,12 +77,14 @@ fc_status fc_polar_workspace_bytes(const fc_polar_desc* desc, size_t* bytes);
 /* Polar Express in place on G (m, n, count) float32 (reference
    src/optim.jl:115-149): X = G (or G^T when m > n) / (1.01 ||G||_F + 1e-6),
    then per step A = X X^T, B = b A + c A A, X = a X + B X, and G = X (or
-   X^T).  The matrix products are strided-batched rocBLAS GEMMs (the
-   reference's CUBLAS gemmStridedBatchedEx, ext/FemtoChatCUDAExt.jl:121-125),
-   with b A and a X folded into the products' beta terms.  The library's
-   rocBLAS handle (one per device, created on the first call) owns rocBLAS's
-   own device workspace; everything else is in the caller's workspace.  Calls
-   from several threads are serialised while they enqueue their GEMMs. */
+   X^T), with b A and a X folded into the products' beta terms (the
+   reference's CUBLAS gemmStridedBatchedEx, ext/FemtoChatCUDAExt.jl:121-125).
+   In bf16 with min(m, n) and max(m, n) multiples of 128 the products are the
+   library's own MFMA kernels (the last one writes G); otherwise they are
+   strided-batched rocBLAS GEMMs, whose handle (one per device, created on
+   the first such call) owns rocBLAS's own device workspace.  Everything else
+   is in the caller's workspace.  Calls from several threads are serialised
+   while they enqueue their products. */
 fc_status fc_polar_express(const fc_polar_desc* desc, float* G, void* workspace, size_t workspace_bytes,
                            void* stream);
 
@@ -90,9 +92,9 @@ fc_status fc_polar_express(const fc_polar_desc* desc, float* G, void* workspace,
    src/optim.jl:278-309, one per matrix shape), each as fc_polar_express with
    its own workspace.  The stacks run concurrently on four helper streams
    forked from and joined back to the caller's stream with events, so the
-   small batched GEMMs of different stacks share the GPU; the helper streams,
-   their rocBLAS handles and the events are created on the first call per
-   device and kept until the process ends. */
+   small batched products of different stacks share the GPU; the helper
+   streams, their rocBLAS handles and the events are created on the first call
+   per device and kept until the process ends. */
 fc_status fc_polar_express_grouped(int32_t count, const fc_polar_desc* descs, float* const* G,
                                    void* const* workspaces, const size_t* workspace_bytes, void* stream);
 

@@ -200,6 +200,20 @@ def test_polar_express_bf16_step_counts(gpu, m, n, steps):
         assert e64 < POLAR_TOL_BF16 and eb < 1.5 * POLAR_TOL_BF16
 
 
+def test_grouped_bf16_many_stacks_equals_separate_calls(gpu):
+    # six stacks on the library's GEMM, more than there are helper streams:
+    # stacks that share a stream run in turn, the others concurrently
+    g = torch.Generator().manual_seed(23)
+    shapes = [(128, 128, 3), (256, 128, 2), (128, 384, 1), (256, 256, 2), (128, 512, 2), (384, 128, 1)]
+    stacks = [torch.randn(k, n, m, generator=g).to(gpu) for m, n, k in shapes]
+    separate = [polar_express(G, compute_type=torch.bfloat16) for G in stacks]
+    grouped = [G.clone() for G in stacks]
+    polar_express_grouped_(grouped, compute_type=torch.bfloat16)
+    torch.cuda.synchronize()
+    for a, b in zip(separate, grouped):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("compute_type", [torch.float32, torch.bfloat16])
 def test_grouped_equals_separate_calls(gpu, compute_type):
     # the stacks run concurrently on helper streams, each with the same GEMMs as

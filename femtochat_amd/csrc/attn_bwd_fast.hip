@@ -8,7 +8,7 @@
 //  * attn_bwd_dkdv_fast: a workgroup owns 128 keys of one (batch, KV head);
 //    each wave keeps its 32 keys' K and V in registers (B operands of
 //    S = Q K^T and dP = dO V^T), loops over the GQA group's heads and the query
-//    tiles (64 queries) that can see the keys, and accumulates dK and dV in
+//    tiles (128 queries) that can see the keys, and accumulates dK and dV in
 //    registers.  Q and dO tiles are staged once into swizzled LDS and read both
 //    as natural fragments (for S, dP) and through ds_read_b64_tr_b16 (for
 //    dV += P^T dO and dK += dS^T Q).

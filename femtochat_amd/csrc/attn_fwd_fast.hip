@@ -4,15 +4,15 @@
 // (src/kernels.jl:131-219; fast-mode rounding of P before P.V and l summed
 // from unrounded probabilities as in ext/FemtoChatCUDAExt.jl:1380-1411).
 //
-// Work split: a workgroup of 4 waves (one per SIMD) owns 256 queries of one
-// (batch, head); each wave owns 64 queries as two 32-query blocks and
-// computes S^T = K Q^T with the query as the lane index, so P^T is directly
-// the B operand of O^T += V^T P^T and every K or V fragment read from LDS
-// feeds two products.  K and V tiles of 128 keys are staged by LDS-DMA into
+// Work split: a workgroup of 4 waves (one per SIMD, two workgroups per CU)
+// owns 128 queries of one (batch, head); each wave owns 32 queries (kWQ; the
+// code allows kNQB 32-query blocks per wave) and computes S^T = K Q^T with
+// the query as the lane index, so P^T is directly the B operand of
+// O^T += V^T P^T.  K and V tiles of 64 keys are staged by LDS-DMA into
 // swizzled LDS (two stages); K is read as natural fragments and V through
 // ds_read_b64_tr_b16, so no transposed copy is written.
 //
-// A tile is processed as four 32-key blocks in a pipeline of six phases:
+// A tile is processed as kNKB 32-key blocks in a pipeline of kNKB + 2 phases:
 // phase i holds the S products of block i, the softmax of block i-1 and the
 // P.V products of block i-2, with one MFMA, a few LDS reads and a few VALU
 // instructions interleaved (sched_group_barrier): at one wave per SIMD a VALU

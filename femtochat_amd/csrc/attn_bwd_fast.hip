@@ -241,7 +241,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
-  const int n_kt = (T + C::kBK - 1) / C::kBK;
   // Key tiles that the most query tiles can see come first.
   const GridItem it0 = heavy_first(blockIdx.x, a.Hkv * a.B);
   const int kt = it0.rank;
@@ -737,7 +736,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
           float ds = p * (dp[bs][r] - dlt);
           if (need_mask) {
             const int kk = kt + 32 * bs + acc_row(r, g);
-            ds = (kk >= lb) & (kk <= ub) & multiple ? ds : 0.0f;
+            ds = ((kk >= lb) & (kk <= ub) & multiple) ? ds : 0.0f;
           }
           dp[bs][r] = ds;
         }

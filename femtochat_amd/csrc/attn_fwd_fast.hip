@@ -65,7 +65,7 @@ __device__ inline void mask_block(f32x16& s, int k0, int g, int lb, int ub) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int c = 8 * (r >> 2) + (r & 3);
-    s[r] = (x >= -c) & (y >= c) ? s[r] : -INFINITY;
+    s[r] = ((x >= -c) & (y >= c)) ? s[r] : -INFINITY;
   }
 }
 

@@ -798,7 +798,7 @@ static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, si
 
 fc_status fc_polar_express(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, void* stream) {
   int dev = 0;
-  hipGetDevice(&dev);
+  if (hipGetDevice(&dev) != hipSuccess) return failf(FC_ERR_HIP, "polar express: hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_blas_mutex);
   rocblas_handle h = blas_handle(dev);
   if (h == nullptr) return failf(FC_ERR_HIP, "polar express: rocblas_create_handle failed");
@@ -814,7 +814,7 @@ fc_status fc_polar_express_grouped(int32_t count, const fc_polar_desc* descs, fl
     if (st != FC_OK) return st;
   }
   int dev = 0;
-  hipGetDevice(&dev);
+  if (hipGetDevice(&dev) != hipSuccess) return failf(FC_ERR_HIP, "polar express grouped: hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_blas_mutex);
   Fork* f = fork_for(dev);
   if (f == nullptr) return failf(FC_ERR_HIP, "polar express grouped: helper streams could not be created");

@@ -170,18 +170,37 @@ __global__ __launch_bounds__(256) void param_copy_kernel(int64_t width, float* s
 }
 
 // ---- Polar Express -------------------------------------------------------------------
-// scale[k] = 1.01 sqrt(sum G_k^2) + 1e-6, summed in float64 in two stages
-// (kNormParts workgroups per matrix write partial sums, then one workgroup
-// per matrix adds them in a fixed order: deterministic).
+// scale[k] = 1.01 sqrt(sum G_k^2) + 1e-6, summed in float64 in two stages:
+// kNormParts workgroups per matrix write partial sums, which the copy into
+// the iteration buffer adds in a fixed order (one wave's butterfly, the same
+// in every workgroup): deterministic.
 constexpr int kNormParts = 64;
 
 __global__ __launch_bounds__(256) void norm_partial_kernel(int64_t size, const float* G, double* partial) {
   __shared__ double part[4];
   const int k = blockIdx.y;
   const float* g = G + (int64_t)k * size;
+  const int64_t stride = (int64_t)kNormParts * 256, i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // 16-byte loads when the matrix is 16-byte aligned (uniform per workgroup),
+  // four loads in flight per thread; a fixed order either way
+  const int64_t nv = (reinterpret_cast<uintptr_t>(g) & 15) == 0 ? size / 4 : 0;
   double s = 0.0;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < size; i += (int64_t)kNormParts * 256)
-    s += (double)g[i] * (double)g[i];
+  int64_t c = i0;
+  for (; c + 3 * stride < nv; c += 4 * stride) {
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = reinterpret_cast<const f32x4*>(g)[c + u * stride];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += (double)v[u][e] * (double)v[u][e];
+  }
+  for (; c < nv; c += stride) {
+    const f32x4 v = reinterpret_cast<const f32x4*>(g)[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s += (double)v[e] * (double)v[e];
+  }
+  for (int64_t i = 4 * nv + i0; i < size; i += stride) s += (double)g[i] * (double)g[i];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = s;
@@ -189,13 +208,6 @@ __global__ __launch_bounds__(256) void norm_partial_kernel(int64_t size, const f
   if (threadIdx.x == 0) partial[k * kNormParts + blockIdx.x] = ((part[0] + part[1]) + part[2]) + part[3];
 }
 
-__global__ __launch_bounds__(64) void norm_finish_kernel(const double* partial, float* scale) {
-  const int k = blockIdx.x;
-  double s = partial[k * kNormParts + threadIdx.x];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-  if (threadIdx.x == 0) scale[k] = 1.01f * sqrtf((float)s) + 1e-6f;
-}
 
 // dst (rows R, cols C, column-major) = src^T / scale (src: C rows, R cols) or
 // src / scale, per matrix (blockIdx.z), through a 32x32 LDS tile; the value
@@ -206,7 +218,24 @@ template <typename T>
 __device__ inline void st(T* p, float v) { *p = static_cast<T>(v); }
 
 template <bool kTranspose, typename S, typename T>
-__global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S* src, T* dst, const float* scale) {
+__global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S* src, T* dst, const double* partial,
+                                                          float* scale_out) {
+  // with partial sums: divide by this matrix's scale (also stored once)
+  __shared__ float s_scale;
+  float sc = 1.0f;
+  if (partial != nullptr) {
+    if (threadIdx.x < 64) {
+      double v = partial[blockIdx.z * kNormParts + threadIdx.x];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      if (threadIdx.x == 0) {
+        s_scale = 1.01f * sqrtf((float)v) + 1e-6f;
+        if (blockIdx.x == 0 && blockIdx.y == 0) scale_out[blockIdx.z] = s_scale;
+      }
+    }
+    __syncthreads();
+    sc = s_scale;
+  }
   __shared__ float tile[32][33];
   const int64_t mat = (int64_t)R * C;
   const S* s = src + blockIdx.z * mat;
@@ -222,14 +251,14 @@ __global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S*
     __syncthreads();
     for (int j = ty; j < 32; j += 8) {
       const int c = c0 + j, r = r0 + tx;
-      if (r < R && c < C) st(d + (int64_t)c * R + r, scale ? tile[tx][j] / scale[blockIdx.z] : tile[tx][j]);
+      if (r < R && c < C) st(d + (int64_t)c * R + r, partial ? tile[tx][j] / sc : tile[tx][j]);
     }
   } else {
     for (int j = ty; j < 32; j += 8) {
       const int c = c0 + j, r = r0 + tx;
       if (r < R && c < C) {
         const float v = ld(s + (int64_t)c * R + r);
-        st(d + (int64_t)c * R + r, scale ? v / scale[blockIdx.z] : v);
+        st(d + (int64_t)c * R + r, partial ? v / sc : v);
       }
     }
   }
@@ -538,6 +567,44 @@ void polar_gemm(bool tr, const PolarGemm& a, int batch, hipStream_t s, int cus) 
   else hipLaunchKernelGGL((polar_gemm_kernel<false, 2>), g, b, 0, s, a);
 }
 
+// The untransposed copy in (m <= n: X has G's layout): X = G / scale per
+// matrix (blockIdx.y), 16-byte loads, the scale from the partial sums as in
+// copy_scaled_kernel.  Needs size % 4 == 0 and 16-byte aligned G and X.
+template <typename T>
+__global__ __launch_bounds__(256) void scale_copy_kernel(int64_t size, const float* G, T* X, const double* partial,
+                                                         float* scale_out) {
+  __shared__ float s_scale;
+  if (threadIdx.x < 64) {
+    double v = partial[blockIdx.y * kNormParts + threadIdx.x];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    if (threadIdx.x == 0) {
+      s_scale = 1.01f * sqrtf((float)v) + 1e-6f;
+      if (blockIdx.x == 0) scale_out[blockIdx.y] = s_scale;
+    }
+  }
+  __syncthreads();
+  const float sc = s_scale;
+  const f32x4* g = reinterpret_cast<const f32x4*>(G + blockIdx.y * size);
+  T* x = X + blockIdx.y * size;
+  const int64_t n4 = size / 4, stride = (int64_t)gridDim.x * 256;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < n4; c += stride) {
+    const f32x4 v = __builtin_nontemporal_load(g + c);
+    if constexpr (sizeof(T) == 2) {
+      typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(v[e] / sc);
+      *reinterpret_cast<bf16x4*>(x + 4 * c) = o;
+    } else {
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = v[e] / sc;
+      *reinterpret_cast<f32x4*>(x + 4 * c) = o;
+    }
+  }
+}
+
 struct PolarLayout {
   size_t X, Y, A, B, scale, partial, total;
 };
@@ -734,16 +801,21 @@ static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, si
 
   hipLaunchKernelGGL(norm_partial_kernel, dim3(kNormParts, k), dim3(256), 0, s, (int64_t)m * n, G, partial);
   if ((st = launched("polar norm")) != FC_OK) return st;
-  hipLaunchKernelGGL(norm_finish_kernel, dim3(k), dim3(64), 0, s, partial, scale);
-  if ((st = launched("polar norm")) != FC_OK) return st;
   // X (lo x hi) = G / scale, or G^T / scale, rounded to the compute type
   const dim3 tiles((lo + 31) / 32, (hi + 31) / 32, k), back((hi + 31) / 32, (lo + 31) / 32, k);
-  if (half) {
-    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, bf16>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<bf16*>(X), scale);
-    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, bf16>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<bf16*>(X), scale);
+  const int64_t msize = (int64_t)m * n;
+  const bool flat = !transposed && msize % 4 == 0 && aligned16(G) && aligned16(X);
+  const dim3 flat_grid((unsigned)std::min<int64_t>((msize / 4 + 255) / 256, std::max<int64_t>(1, 2048 / k)), k);
+  if (flat && half) {
+    hipLaunchKernelGGL(scale_copy_kernel<bf16>, flat_grid, dim3(256), 0, s, msize, G, reinterpret_cast<bf16*>(X), partial, scale);
+  } else if (flat) {
+    hipLaunchKernelGGL(scale_copy_kernel<float>, flat_grid, dim3(256), 0, s, msize, G, reinterpret_cast<float*>(X), partial, scale);
+  } else if (half) {
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, bf16>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<bf16*>(X), partial, scale);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, bf16>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<bf16*>(X), partial, scale);
   } else {
-    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, float>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<float*>(X), scale);
-    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<float*>(X), scale);
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, float>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<float*>(X), partial, scale);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, G, reinterpret_cast<float*>(X), partial, scale);
   }
   if ((st = launched("polar copy in")) != FC_OK) return st;
 
@@ -791,11 +863,11 @@ static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, si
   }
   // G = X, or X^T (widened to fp32)
   if (half) {
-    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, bf16, float>), back, dim3(256), 0, s, hi, lo, reinterpret_cast<const bf16*>(X), G, nullptr);
-    else hipLaunchKernelGGL((copy_scaled_kernel<false, bf16, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const bf16*>(X), G, nullptr);
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, bf16, float>), back, dim3(256), 0, s, hi, lo, reinterpret_cast<const bf16*>(X), G, nullptr, nullptr);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, bf16, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const bf16*>(X), G, nullptr, nullptr);
   } else {
-    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, float>), back, dim3(256), 0, s, hi, lo, reinterpret_cast<const float*>(X), G, nullptr);
-    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const float*>(X), G, nullptr);
+    if (transposed) hipLaunchKernelGGL((copy_scaled_kernel<true, float, float>), back, dim3(256), 0, s, hi, lo, reinterpret_cast<const float*>(X), G, nullptr, nullptr);
+    else hipLaunchKernelGGL((copy_scaled_kernel<false, float, float>), tiles, dim3(256), 0, s, lo, hi, reinterpret_cast<const float*>(X), G, nullptr, nullptr);
   }
   return launched("polar copy out");
 }

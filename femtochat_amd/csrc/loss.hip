@@ -196,7 +196,8 @@ __global__ __launch_bounds__(256) void xent_bwd_kernel(XentArgs a) {
           const float p = exp2f((x[k][i] - lse) * kLog2e);
           g[i] = w * (p - (4 * c + i == t ? 1.0f : 0.0f));
         }
-        *reinterpret_cast<f32x4*>(out + 4 * c) = a.overwrite ? g : o[k] + g;
+        // nontemporal store (1.6% faster here; not in the fused kernel, where it was slower)
+        __builtin_nontemporal_store(a.overwrite ? g : o[k] + g, reinterpret_cast<f32x4*>(out + 4 * c));
       }
     }
   } else {

@@ -133,6 +133,28 @@ def test_polar_express_matches_oracle(gpu, m, n, k):
         np.testing.assert_allclose(np.sort(s_out), np.sort(O.composed_polynomial(s_in / scale)), atol=POLAR_TOL * 4)
 
 
+@pytest.mark.parametrize("m,n,k,compute_type", [(7, 13, 3, torch.float32), (13, 7, 2, torch.float32), (1, 5, 2, torch.float32),
+                                                 (31, 45, 2, torch.bfloat16), (45, 31, 2, torch.bfloat16),
+                                                 (33, 97, 1, torch.bfloat16)])
+def test_polar_express_odd_sizes(gpu, m, n, k, compute_type):
+    # m n not a multiple of 4: the copy into the iteration buffer takes its
+    # element-wise path (the 16-byte one needs whole 16-byte groups).  bf16 at
+    # a few tens of rows: below that one element's rounding, amplified by the
+    # first steps' cancellations (coefficients up to 22), decides the max norm.
+    g = torch.Generator().manual_seed(m * 11 + n)
+    G = torch.randn(k, n, m, generator=g)
+    out = polar_express(G.to(gpu), compute_type=compute_type).cpu()
+    ref = O.polar_express(G.numpy().transpose(0, 2, 1)).transpose(0, 2, 1)
+    e64 = rel_err(out.numpy(), ref)
+    emu = (_torch_polar_f32 if compute_type == torch.float32 else _torch_polar_bf16)(G.to(gpu)).cpu().numpy()
+    say(f"polar {compute_type} {m}x{n}x{k}: vs float64 {e64:.2e}, vs torch {rel_err(out.numpy(), emu):.2e}")
+    if compute_type == torch.float32:
+        assert e64 < POLAR_TOL and rel_err(out.numpy(), emu) < POLAR_TOL
+    else:  # as the other bf16 cases: no further from float64 than the reference's own bf16 iteration allows
+        e_ref = rel_err(emu, ref)
+        assert e64 <= max(POLAR_TOL_BF16, 1.5 * e_ref)
+
+
 def _torch_polar_bf16(G):
     """The reference's bf16 iteration in plain torch: bf16 buffers, fp32 scalars
     and elementwise arithmetic, products rounded to bf16."""

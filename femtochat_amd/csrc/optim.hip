@@ -272,9 +272,11 @@ __global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S*
 //   C, D  column-major M x N (leading dimension M)
 // A workgroup of four waves computes a 128 x 128 tile of D, each wave 64 x 64
 // as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16.  The k loop runs in steps of
-// 64 through two LDS stages filled by direct global->LDS loads (the next
-// step's loads are in flight while the current step's products run; one
-// barrier per step):
+// 64 through kStages LDS stages filled by direct global->LDS loads (two, at
+// two workgroups per CU; three, at one, when the grid leaves CUs free): the
+// next kStages - 1 steps' loads are in flight while a step's products run,
+// with one barrier per step.  The fragment reads of each 16-wide chunk are
+// issued ahead of the previous chunk's products.  Tiles:
 //   * kTr: k-major tiles (64 rows of k, 128 values of i or j, 256 B per row,
 //     the 16-byte units of row r XOR-swizzled by 4(r mod 4) + (r/4 mod 4)),
 //     read with ds_read_b64_tr_b16, four k of one column per 8-byte read;
@@ -283,6 +285,9 @@ __global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S*
 //     reads take about twice as long for the same bytes).
 // Both reads are free of bank conflicts and give lane l (g = l/32) the column
 // l mod 32 and k = 8g + e, e < 8, so P and Q fragments pair in the MFMA.
+// The epilogue leaves through LDS: each wave writes its fp32 quadrant by
+// column (padded), then eight lanes cover one 128-byte column segment of D,
+// adding beta C (loaded in that layout before the k loop) and rounding once.
 // M, N multiples of 128, K a multiple of 64, every operand under 2^31 bytes
 // (checked by the caller): all tiles are whole and every offset is 32-bit.
 struct PolarGemm {

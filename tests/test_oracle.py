@@ -166,6 +166,28 @@ def test_gqa_equals_repeated_kv_and_permutation():
     assert np.allclose(Op, O[p], atol=1e-14)
 
 
+@pytest.mark.parametrize("case", CASES, ids=[str(c[0]) for c in CASES])
+def test_backward_sum_identities(case):
+    # The whole-output identities the full-size GPU tests check: each query's
+    # probabilities sum to one over its visible keys and its dS row to zero,
+    # so per (batch, KV head) sum_t dV = the group's sum_t dO and sum_t dK = 0.
+    # A planted mistake (one key block's dV and dK dropped) must break both.
+    seed, B, T, H, Hkv, D, window, pos_kind = case
+    Q, K, V, dO = rand(seed, B, T, H, Hkv, D)
+    pos = _positions(seed, B, T) if pos_kind == "docs" else None
+    O, l, m = R.forward(Q, K, V, window, pos)
+    dQ, dK, dV = R.backward(dO, Q, K, V, O, l, m, window, pos)
+    G = H // Hkv
+    dO_sum = dO.reshape(B, T, Hkv, G, D).sum(axis=(1, 3))
+    assert np.allclose(dV.sum(axis=1), dO_sum, atol=1e-12 * np.abs(dO).sum())
+    assert np.all(np.abs(dK.sum(axis=1)) <= 1e-12 * np.abs(dK).sum(axis=1) + 1e-300)
+    dV_bad, dK_bad = dV.copy(), dK.copy()
+    dV_bad[:, :4] = 0.0
+    dK_bad[:, :4] = 0.0
+    assert np.max(np.abs(dV_bad.sum(axis=1) - dO_sum)) > 1e-3 * np.max(np.abs(dO_sum))
+    assert np.max(np.abs(dK_bad.sum(axis=1)) / np.abs(dK).sum(axis=1)) > 1e-3
+
+
 def test_document_mask_equals_segments():
     T, H, Hkv, D = 30, 2, 1, 16
     lengths = [7, 1, 12, 10]

@@ -203,6 +203,24 @@ def measure_loss(dev, steps: int) -> dict:
         out[name] = {"ms": round(ms, 4), "launches": n, "bytes": nbytes,
                      "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                                   "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}}
+    # the deterministic gradient (key kernel, radix sort passes, one in-order
+    # sum per id), timed with events around the whole call
+    from femtochat_amd.loss import embedding_gradient_workspace_bytes
+    ws = torch.empty(embedding_gradient_workspace_bytes(dW, tokens), dtype=torch.uint8, device=dev)
+    for _ in range(3):
+        embedding_gradient_(dW, dY, tokens, deterministic=True, workspace=ws)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        embedding_gradient_(dW, dY, tokens, deterministic=True, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    achieved = 3 * em / (ms * 1e-3) / 1e9
+    out["embed_bwd_sorted"] = {"ms": round(ms, 4), "bytes": 3 * em, "deterministic": True,
+                               "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                                            "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}}
     return out
 
 

@@ -179,6 +179,8 @@ _SIGNATURES = {
     "fc_cross_entropy_fused": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "fc_embedding_fwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
     "fc_embedding_bwd": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P]),
+    "fc_embedding_bwd_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), ctypes.POINTER(ctypes.c_size_t)]),
+    "fc_embedding_bwd_sorted": (ctypes.c_int, [ctypes.POINTER(EmbedDesc), _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "fc_xla_bind_attention_fwd": (ctypes.c_void_p, [ctypes.POINTER(AttnDesc), ctypes.c_int32]),
     "fc_xla_bind_attention_bwd": (ctypes.c_void_p, [ctypes.POINTER(AttnDesc), ctypes.c_int32,
                                                     ctypes.POINTER(ctypes.c_size_t)]),

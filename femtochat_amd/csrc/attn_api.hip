@@ -527,6 +527,39 @@ fc_status fc_embedding_bwd(const fc_embed_desc* desc, float* dweights, const voi
   return ok();
 }
 
+fc_status fc_embedding_bwd_workspace_bytes(const fc_embed_desc* desc, size_t* bytes) {
+  fc::EmbedArgs a;
+  static const int64_t no_tokens = 0;  // the query reads no tokens (aligned for either index type)
+  const fc_status st = embed_args(desc, &no_tokens, "fc_embedding_bwd_workspace_bytes", &a);
+  if (st != FC_OK) return st;
+  if (bytes == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_bwd_workspace_bytes: bytes is null");
+  if (desc->N >= ((int64_t)1 << 31)) return fail(FC_ERR_UNSUPPORTED, "fc_embedding_bwd_workspace_bytes: at most 2^31 - 1 tokens");
+  *bytes = fc::embed_sort_layout(desc->N, desc->vocab).total;
+  return ok();
+}
+
+fc_status fc_embedding_bwd_sorted(const fc_embed_desc* desc, float* dweights, const void* dy, const void* tokens,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  fc::EmbedArgs a;
+  const fc_status st = embed_args(desc, tokens, "fc_embedding_bwd_sorted", &a);
+  if (st != FC_OK) return st;
+  if (dweights == nullptr || dy == nullptr)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_bwd_sorted: dweights and dy are required");
+  if (!aligned4(dweights) || (reinterpret_cast<uintptr_t>(dy) & (desc->y_dtype == FC_BF16 ? 1 : 3)) != 0)
+    return fail(FC_ERR_INVALID_ARGUMENT, "fc_embedding_bwd_sorted: buffers are not aligned to their element size");
+  if (desc->N >= ((int64_t)1 << 31)) return fail(FC_ERR_UNSUPPORTED, "fc_embedding_bwd_sorted: at most 2^31 - 1 tokens");
+  const size_t need = fc::embed_sort_layout(desc->N, desc->vocab).total;
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(FC_ERR_WORKSPACE, "fc_embedding_bwd_sorted needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(FC_ERR_WORKSPACE, "fc_embedding_bwd_sorted: workspace must be 256-byte aligned");
+  a.dweights = dweights;
+  a.dy = dy;
+  const hipError_t e = fc::launch_embed_sorted(a, desc->y_dtype == FC_BF16, workspace, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "sorted embedding gradient launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 fc_status fc_capabilities(int32_t device, fc_caps* caps) {
   if (caps == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "caps is null");
   hipDeviceProp_t prop;

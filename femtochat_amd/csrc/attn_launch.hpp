@@ -153,6 +153,15 @@ struct EmbedArgs {
 };
 hipError_t launch_embed(const EmbedArgs& a, bool backward, bool bf16_y, hipStream_t s);
 
+// Workspace of the sorted (deterministic) embedding gradient: keys and token
+// indices before and after the sort, and the sort's own temporary storage
+// (byte offsets, 256-aligned).
+struct EmbedSortLayout {
+  size_t key_in, key_out, val_in, val_out, temp, temp_bytes, total;
+};
+EmbedSortLayout embed_sort_layout(int64_t N, int vocab);
+hipError_t launch_embed_sorted(const EmbedArgs& a, bool bf16_dy, void* workspace, hipStream_t s);
+
 // Workspace layout of the backward pass (byte offsets, 256-aligned).
 struct BwdWorkspace {
   size_t delta, lse2, chunk_lb, dO16, total;

@@ -39,6 +39,7 @@ __all__ = [
     "embedding",
     "embedding_",
     "embedding_gradient_",
+    "embedding_gradient_workspace_bytes",
     "EmbeddingFunction",
 ]
 
@@ -230,12 +231,33 @@ def embedding(weights: torch.Tensor, tokens: torch.Tensor, out_dtype: Optional[t
     return y
 
 
-def embedding_gradient_(dweights: torch.Tensor, dy: torch.Tensor, tokens: torch.Tensor, *, index_base: int = 0) -> None:
-    """dweights[tokens[t], :] += dy[t, :] (src/kernels.jl:8-14), fp32 atomics."""
+def embedding_gradient_workspace_bytes(dweights: torch.Tensor, tokens: torch.Tensor, dy_dtype=torch.float32) -> int:
+    """Workspace bytes of ``embedding_gradient_(..., deterministic=True)``."""
+    d = _embed_desc(dweights, tokens, dy_dtype, 0)
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fc_embedding_bwd_workspace_bytes(ctypes.byref(d), ctypes.byref(n)))
+    return n.value
+
+
+def embedding_gradient_(dweights: torch.Tensor, dy: torch.Tensor, tokens: torch.Tensor, *, index_base: int = 0,
+                        deterministic: bool = False, workspace: Optional[torch.Tensor] = None) -> None:
+    """dweights[tokens[t], :] += dy[t, :] (src/kernels.jl:8-14): fp32 atomics
+    (the reference's order-free adds), or with ``deterministic=True`` a sort
+    by id and one in-order sum per id (the same bits on every call; the
+    workspace, uint8 of ``embedding_gradient_workspace_bytes`` bytes, is
+    allocated here when not given)."""
     d = _embed_desc(dweights, tokens, dy.dtype, index_base)
     _check_tensor("dy", dy, tuple(tokens.shape) + (dweights.shape[1],), (torch.float32, torch.bfloat16), dweights.device)
-    _lib.check(_lib.lib().fc_embedding_bwd(ctypes.byref(d), _ptr(dweights), _ptr(dy), _ptr(tokens),
-                                           _stream_ptr(dweights.device)))
+    if not deterministic:
+        _lib.check(_lib.lib().fc_embedding_bwd(ctypes.byref(d), _ptr(dweights), _ptr(dy), _ptr(tokens),
+                                               _stream_ptr(dweights.device)))
+        return
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fc_embedding_bwd_workspace_bytes(ctypes.byref(d), ctypes.byref(n)))
+    if workspace is None:
+        workspace = torch.empty(n.value, dtype=torch.uint8, device=dweights.device)
+    _lib.check(_lib.lib().fc_embedding_bwd_sorted(ctypes.byref(d), _ptr(dweights), _ptr(dy), _ptr(tokens),
+                                                  _ptr(workspace), workspace.numel(), _stream_ptr(dweights.device)))
 
 
 class EmbeddingFunction(torch.autograd.Function):

@@ -16,6 +16,7 @@
 #ifndef FEMTOCHAT_LOSS_H
 #define FEMTOCHAT_LOSS_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include "femtochat_attn.h"
@@ -98,6 +99,21 @@ fc_status fc_embedding_fwd(const fc_embed_desc* desc, const float* weights, cons
    ext/FemtoChatCUDAExt.jl:78-94). */
 fc_status fc_embedding_bwd(const fc_embed_desc* desc, float* dweights, const void* dy, const void* tokens,
                            void* stream);
+
+/* Bytes of the caller-owned workspace of fc_embedding_bwd_sorted for these
+   N and vocab (the sort's keys and token indices and its temporary storage). */
+fc_status fc_embedding_bwd_workspace_bytes(const fc_embed_desc* desc, size_t* bytes);
+
+/* The gradient of fc_embedding_bwd, deterministic: the tokens are sorted by
+   id (a stable device radix sort), and each id's dy columns are summed in
+   token order, skipping zero values, from -0; the sum is then added to
+   dweights[:, id] once.  The same inputs give the same bits on every call,
+   with no atomics.  workspace: at least fc_embedding_bwd_workspace_bytes,
+   256-byte aligned.  No reference counterpart as one call: the reference's
+   embedding_gradient! (src/kernels.jl:8-14; CUDA ext/FemtoChatCUDAExt.jl:78-94)
+   adds with atomics in no fixed order. */
+fc_status fc_embedding_bwd_sorted(const fc_embed_desc* desc, float* dweights, const void* dy, const void* tokens,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

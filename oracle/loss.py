@@ -94,3 +94,29 @@ def embedding_gradient(delta, dy, tokens, base: int = 1) -> np.ndarray:
     out = np.array(delta, dtype=np.float64, copy=True)
     np.add.at(out, np.asarray(tokens).astype(np.int64) - base, np.asarray(dy, dtype=np.float64))
     return out
+
+
+def embedding_gradient_in_order_f32(delta, dy, tokens, base: int = 1) -> np.ndarray:
+    """The same gradient in one fixed float32 order: per id, its dy rows summed
+    in token order (zero values skipped, from -0), the sum added to delta once;
+    ids outside the table add nothing.  The reference's atomic adds
+    (CUDAExt:78-94) have no order; this is the order of the library's
+    deterministic gradient, whose bits it must match.  Its sums equal
+    embedding_gradient's within float32 rounding."""
+    out = np.array(delta, dtype=np.float32, copy=True)
+    ids = np.asarray(tokens).astype(np.int64) - base
+    dy = np.asarray(dy, dtype=np.float32)
+    order = np.argsort(ids, kind="stable")
+    sorted_ids = ids[order]
+    heads = np.flatnonzero(np.r_[True, sorted_ids[1:] != sorted_ids[:-1]])
+    ends = np.r_[heads[1:], len(ids)]
+    for h, e in zip(heads, ends):
+        i = sorted_ids[h]
+        if i < 0 or i >= out.shape[0]:
+            continue
+        s = np.full(out.shape[1], -0.0, np.float32)
+        for t in order[h:e]:
+            v = dy[t]
+            s = np.where(v != 0, (s + v).astype(np.float32), s)
+        out[i] = (out[i] + s).astype(np.float32)
+    return out

@@ -233,6 +233,57 @@ def test_embedding_gradient_matches_oracle(gpu, dy_dtype, D):
     assert torch.equal(dW2.cpu(), exact)
 
 
+@pytest.mark.parametrize("dy_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("itype,base", [(torch.int32, 0), (torch.int64, 1)])
+@pytest.mark.parametrize("D", [1, 37, 512, 600])
+def test_sorted_embedding_gradient_is_bit_exact(gpu, dy_dtype, itype, base, D):
+    # the deterministic gradient sums each id's rows in token order and adds
+    # once: it must equal the oracle's float32 restatement of that order bit
+    # for bit (repeats, zero values, signed zeros, ids outside the table)
+    g = torch.Generator().manual_seed(D * 3 + base)
+    vocab, N = 50, 700
+    tok = torch.randint(0, vocab, (N,), generator=g)
+    tok[:80] = 9                       # one heavily repeated id
+    tok[100:103] = torch.tensor([-1, vocab, 3 * vocab])  # outside the table (after the base shift)
+    dy = torch.randn(N, D, generator=g).to(dy_dtype)
+    dy[200:220] = 0.0                  # zero values are skipped
+    dy[230, : min(D, 5)] = -0.0
+    delta = torch.randn(vocab, D, generator=g)
+    delta[::7] = -0.0                  # a column receiving only zeros keeps its bits
+    dW = delta.to(gpu)
+    tokens = (tok + base).to(itype)
+    embedding_gradient_(dW, dy.to(gpu), tokens.to(gpu), index_base=base, deterministic=True)
+    exact = O.embedding_gradient_in_order_f32(delta.numpy(), dy.float().numpy(), tokens.numpy(), base=base)
+    got = dW.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), exact.view(np.uint32))
+    # and the mathematics: within float32 rounding of the float64 sums
+    keep = (tok >= 0) & (tok < vocab)
+    ref = O.embedding_gradient(delta.numpy(), dy.float().numpy()[keep.numpy()], tok[keep].numpy(), base=0)
+    assert rel_err(got - delta.numpy(), ref - delta.numpy()) < 1e-5
+
+
+def test_sorted_embedding_gradient_training_size(gpu):
+    # scripts/train.jl's shape (4 x 2048 tokens, 512 wide, vocabulary 2^15):
+    # the same bits on every call, the order's exact sums, and the atomic
+    # gradient within float32 rounding
+    g = torch.Generator().manual_seed(5)
+    vocab, N, D = 32768, 8192, 512
+    tok = torch.randint(0, vocab, (N,), generator=g, dtype=torch.int32)
+    tok[:1000] = 17
+    dy = torch.randn(N, D, generator=g)
+    runs = []
+    for _ in range(2):
+        dW = torch.zeros(vocab, D, device=gpu)
+        embedding_gradient_(dW, dy.to(gpu), tok.to(gpu), deterministic=True)
+        runs.append(dW.cpu())
+    assert torch.equal(runs[0], runs[1])
+    exact = O.embedding_gradient_in_order_f32(np.zeros((vocab, D), np.float32), dy.numpy(), tok.numpy(), base=0)
+    assert np.array_equal(runs[0].numpy().view(np.uint32), exact.view(np.uint32))
+    dA = torch.zeros(vocab, D, device=gpu)
+    embedding_gradient_(dA, dy.to(gpu), tok.to(gpu))
+    assert torch.allclose(dA.cpu(), runs[0], rtol=1e-5, atol=1e-4)
+
+
 def test_autograd_embedding(gpu):
     W = torch.randn(50, 24)
     tok = torch.randint(0, 50, (4, 11))

@@ -77,6 +77,31 @@ def test_closed_forms():
                                rtol=1e-9, atol=1e-9)
 
 
+def test_in_order_embedding_gradient():
+    # the fixed-order float32 gradient equals the float64 one within float32
+    # rounding, skips ids outside the table, and leaves a column that receives
+    # only zeros (and a -0 in it) with its bits
+    rng = np.random.default_rng(3)
+    vocab, N, D = 20, 200, 6
+    tok = rng.integers(0, vocab, N)
+    tok[:5] = [-1, vocab, 4, 4, 4]
+    dy = rng.standard_normal((N, D)).astype(np.float32)
+    dy[tok == 11] = 0.0
+    delta = rng.standard_normal((vocab, D)).astype(np.float32)
+    delta[11, 0] = -0.0
+    out = L.embedding_gradient_in_order_f32(delta, dy, tok, base=0)
+    keep = (tok >= 0) & (tok < vocab)
+    ref = L.embedding_gradient(delta, dy[keep], tok[keep], base=0)
+    assert np.allclose(out, ref, rtol=1e-5, atol=1e-5)
+    assert np.array_equal(out[11].view(np.uint32), delta[11].view(np.uint32))
+    # order matters in float32: a planted reverse order changes some bits
+    # when a run's values differ widely in magnitude
+    big = np.zeros((3, 1), np.float32)
+    rows = np.array([[1e8], [1.0], [-1e8]], np.float32)
+    fwd = L.embedding_gradient_in_order_f32(big, rows, np.array([0, 0, 0]), base=0)
+    assert fwd[0, 0] == 0.0  # (1e8 + 1) rounds to 1e8, minus 1e8 is 0, in this order
+
+
 def test_embedding_matches_torch():
     rng = np.random.default_rng(6)
     W = rng.standard_normal((50, 12))

@@ -18,6 +18,11 @@ What is restated (citations into msjgriffiths/femtochat):
   (src/gpt.jl:34; CUDAExt:63-76), a gather of weight columns.
 * ``embedding_gradient``     : ``embedding_gradient!`` (src/kernels.jl:8-14,
   CUDAExt:78-94): delta[:, tokens[t]] += dy[:, t].
+* ``embedding_gradient_in_order_f32``: the same sums in one fixed float32
+  order (per id, token order, zero values skipped, added once), the order of
+  the library's deterministic gradient; pinned against ``embedding_gradient``
+  within float32 rounding, a column receiving only zeros keeping its bits,
+  and a cancellation that only that order gives.
 
 Layout (torch, row-major): logits (N, V) with N tokens (the reference's
 (V, T, B) column-major array), targets (N,), embedding weights (vocab, D)

@@ -109,7 +109,9 @@ fc_status fc_embedding_bwd_workspace_bytes(const fc_embed_desc* desc, size_t* by
    token order, skipping zero values, from -0; the sum is then added to
    dweights[:, id] once.  The same inputs give the same bits on every call,
    with no atomics.  workspace: at least fc_embedding_bwd_workspace_bytes,
-   256-byte aligned.  No reference counterpart as one call: the reference's
+   256-byte aligned.  The sort (rocPRIM's device radix sort) clears its
+   counters with hipMemsetAsync, so this call is not for HIP graph capture
+   (fc_embedding_bwd is).  No reference counterpart as one call: the reference's
    embedding_gradient! (src/kernels.jl:8-14; CUDA ext/FemtoChatCUDAExt.jl:78-94)
    adds with atomics in no fixed order. */
 fc_status fc_embedding_bwd_sorted(const fc_embed_desc* desc, float* dweights, const void* dy, const void* tokens,

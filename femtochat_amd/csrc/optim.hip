@@ -27,6 +27,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #pragma clang fp contract(off)
@@ -347,28 +348,55 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <bool kTr, int kStages>
+// kNarrow (with kTr, for A = X X^T when 128 x 128 tiles would not fill the
+// CUs): 128 x 64 tiles, each wave 64 x 32 (2 x 1 blocks); the Q tile is 64
+// rows of k by 64 values (128 B per row, units swizzled by 4 ((r/2) mod 2),
+// which keeps its transposed reads free of bank conflicts).
+template <bool kTr, int kStages, bool kNarrow = false>
 __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(PolarGemm a) {
-  // kStages stages of [P, Q] tiles; after the k loop, each wave's 64 x 64
+  static_assert(!kNarrow || kTr, "narrow tiles are for the k-major products");
+  constexpr int kTN = kNarrow ? 64 : kGemmTile;  // tile width (j)
+  constexpr int kNY = kTN / 64;                   // 32-column blocks per wave
+  constexpr int kQBytes = kNarrow ? 8192 : 16384;
+  constexpr int kStageBytes = 16384 + kQBytes;
+  // kStages stages of [P, Q] tiles; after the k loop, each wave's 64 x 32 kNY
   // fp32 quadrant (columns of kQuadPitch bytes)
-  constexpr int kLds = 32768 * kStages > 4 * kQuadBytes ? 32768 * kStages : 4 * kQuadBytes;
+  constexpr int kLds = kStageBytes * kStages > 4 * kQuadBytes ? kStageBytes * kStages : 4 * kQuadBytes;
   __shared__ __attribute__((aligned(1024))) char lds[kLds];
-  auto tile = [&](int stage, int which) __attribute__((always_inline)) { return lds + 32768 * stage + 16384 * which; };
-  const int tm = a.M / kGemmTile, tiles = tm * (a.N / kGemmTile);
+  auto tile = [&](int stage, int which) __attribute__((always_inline)) { return lds + kStageBytes * stage + 16384 * which; };
+  const int tm = a.M / kGemmTile, tiles = tm * (a.N / kTN);
   // XCD-aware order: workgroup w runs on XCD w mod 8, so the eight XCDs take
   // contiguous runs of tiles (whole matrices, sharing operands in their L2)
   int w = blockIdx.x;
   if ((gridDim.x & 7) == 0) w = (w & 7) * (gridDim.x >> 3) + (w >> 3);
   const int b = w / tiles, t = w - b * tiles;
-  const int i0 = (t % tm) * kGemmTile, j0 = (t / tm) * kGemmTile;
+  const int i0 = (t % tm) * kGemmTile, j0 = (t / tm) * kTN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wi = wave & 1, wj = wave >> 1, l32 = lane & 31, g = lane >> 5;
 
   const u32x4s pw = buffer_words(a.P + b * a.sp, (uint32_t)((int64_t)(kTr ? a.K : a.M) * a.ldp * 2));
   const u32x4s qw = buffer_words(a.Q + b * a.sq, (uint32_t)((int64_t)(kTr ? a.K : a.N) * a.ldq * 2));
   using Dma = GemmDma<kTr ? 16 : 8>;
-  Dma pdma, qdma;
+  Dma pdma;
   pdma.init(wave, lane, 2 * a.ldp);
+  // the narrow Q tile: 8 blocks of 1 KB, two per wave, block b at 64 b + lane
+  // units, 8 units per row
+  struct NarrowDma {
+    int goff[2];
+    __device__ inline void init(int wave, int lane, int pitch_bytes) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int unit = 64 * (wave + kWaves * j) + lane, row = unit / 8, pu = unit % 8;
+        goff[j] = row * pitch_bytes + 16 * (pu ^ (4 * ((row >> 1) & 1)));
+      }
+    }
+    __device__ inline void issue(u32x4s words, int tile_off, uint32_t lds, int wave) const {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        dma_load16(words, goff[j] + tile_off, __builtin_amdgcn_readfirstlane(lds + 1024 * (wave + kWaves * j)));
+    }
+  };
+  typename std::conditional<kNarrow, NarrowDma, Dma>::type qdma;
   qdma.init(wave, lane, 2 * a.ldq);
   // tile origin of k step s: rows 64s, columns i0 (P) or j0 (Q) when kTr,
   // else rows i0 or j0, columns 64s
@@ -379,13 +407,14 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
 
   // fragment offsets: k-major tiles (rows 8g + 4e + a, a = (lane mod 16)/4,
   // column 16 ((lane/16) mod 2) + 4 (lane mod 4), +64 B per 32-column block)
-  int tr[2];
+  int tr[2], trn[2];  // 256-byte rows (P, wide Q); 128-byte rows (narrow Q, wave's block 4 wj units in)
   {
     const int s = lane & 15, ar = s >> 2, cc = s & 3, u = 2 * ((lane >> 4) & 1) + (cc >> 1);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int r = 8 * g + 4 * e + ar;
       tr[e] = 256 * r + 16 * (u ^ gemm_swz<16>(r)) + 8 * (cc & 1);
+      trn[e] = 128 * r + 16 * ((4 * wj + u) ^ (4 * ((r >> 1) & 1))) + 8 * (cc & 1);
     }
   }
   // i- or j-major tiles: row 64 wi + 32 x + l32 (P) or 64 wj + 32 y + l32 (Q),
@@ -393,11 +422,11 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
   const int nat = l32 * 128 + 16 * (g ^ gemm_swz<8>(l32));
   const int natp = nat + 64 * 128 * wi, natq = nat + 64 * 128 * wj;
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][kNY];
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y)
+    for (int y = 0; y < kNY; ++y)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.0f;
 
@@ -410,16 +439,17 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
   const bool has_c = a.beta != 0.0f;  // without C the loads read zero records: no memory access
   const auto rc = make_rsrc(has_c ? a.C + b * a.sd : a.D, has_c ? (uint32_t)dbytes : 0u);
   const auto rg = make_rsrc(a.gmode != 0 ? static_cast<const void*>(a.G + b * (int64_t)a.M * a.N) : a.D, a.gmode != 0 ? (uint32_t)(2 * dbytes) : 0u);
-  const int orow = 64 * wi + 8 * (lane & 7), ocol = 64 * wj + (lane >> 3);
+  const int orow = 64 * wi + 8 * (lane & 7), ocol = 32 * kNY * wj + (lane >> 3);
   auto out_off = [&](int t) __attribute__((always_inline)) { return 2 * ((j0 + ocol + 8 * t) * a.M + i0 + orow); };
-  u32x4 cw[8];
+  constexpr int kPasses = 4 * kNY;
+  u32x4 cw[kPasses];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) cw[t] = __builtin_amdgcn_raw_buffer_load_b128(rc, out_off(t), 0, 0);
+  for (int t = 0; t < kPasses; ++t) cw[t] = __builtin_amdgcn_raw_buffer_load_b128(rc, out_off(t), 0, 0);
 
   // k steps s .. s + kStages - 2 are in flight while step s is multiplied
   // (each wave issues kDmaPer loads per step); a step's stage is refilled
   // after the barrier that follows every wave's last read of it
-  constexpr int kDmaPer = 2 * Dma::kPer;
+  constexpr int kDmaPer = Dma::kPer + (kNarrow ? 2 : Dma::kPer);
   const int steps = a.K / kGemmK;
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
@@ -433,7 +463,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
     const char* pt = tile(stage, 0);
     const char* qt = tile(stage, 1);
     // fragments of chunk c + 1 are read while chunk c's products run
-    bf16x8 pf[2][2], qf[2][2];
+    bf16x8 pf[2][2], qf[2][kNY];
     auto read = [&](int c, bf16x8* p, bf16x8* q) __attribute__((always_inline)) {
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
@@ -445,8 +475,10 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
         }
       }
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        if (kTr) {
+      for (int y = 0; y < kNY; ++y) {
+        if (kNarrow) {
+          q[y] = lds_tr_frag(qt, trn[0] + 2048 * c, trn[1] + 2048 * c);
+        } else if (kTr) {
           const int blk = 128 * wj + 64 * y;
           q[y] = lds_tr_frag(qt, (tr[0] + 4096 * c) ^ blk, (tr[1] + 4096 * c) ^ blk);
         } else {
@@ -461,19 +493,19 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int y = 0; y < 2; ++y)
+        for (int y = 0; y < kNY; ++y)
           acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf[c & 1][x], qf[c & 1][y], acc[x][y], 0, 0, 0);
     }
     // keep that order through scheduling: LDS reads of chunk c + 1 ahead of
     // the products of chunk c (masks: 0x100 LDS read, 0x008 MFMA)
-    constexpr int kReads = kTr ? 8 : 4;
+    constexpr int kReads = kTr ? 4 + 2 * kNY : 4;
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
     for (int c = 0; c < kGemmK / 16 - 1; ++c) {
       __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNY, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNY, 0);
   }
   __syncthreads();  // every wave's last reads of the stages precede the quadrant writes
 
@@ -483,7 +515,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y)
+    for (int y = 0; y < kNY; ++y)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         f32x4 v;
@@ -497,7 +529,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
            ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
   };
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int t = 0; t < kPasses; ++t) {
     const char* src = quad + (8 * t + (lane >> 3)) * kQuadPitch + 32 * (lane & 7);
     const f32x4 lo4 = *reinterpret_cast<const f32x4*>(src), hi4 = *reinterpret_cast<const f32x4*>(src + 16);
     float v[8] = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
@@ -526,17 +558,19 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
     }
   }
   if (a.gmode == 2) {
-    // lane l, pass t: quadrant row 8t + l/8, columns 8 (l mod 8) .. +7, i.e.
-    // 32 contiguous bytes of a row of G^T (eight lanes: one 256-byte row segment)
+    // lane l, pass t: quadrant row (64/kLpr) t + l/kLpr, columns 8 (l mod kLpr)
+    // .. +7, i.e. 32 contiguous bytes of a row of G^T (kLpr lanes: one row
+    // segment of the quadrant's width)
     __syncthreads();
-    const int c0 = 8 * (lane & 7);
+    constexpr int kLpr = 4 * kNY;
+    const int c0 = 8 * (lane % kLpr);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int r = 8 * t + (lane >> 3);
+    for (int t = 0; t < kPasses; ++t) {
+      const int r = (64 / kLpr) * t + lane / kLpr;
       float v[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = *reinterpret_cast<const float*>(quad + (c0 + e) * kQuadPitch + 4 * r);
-      const int goff = 4 * ((i0 + 64 * wi + r) * a.N + j0 + 64 * wj + c0);
+      const int goff = 4 * ((i0 + 64 * wi + r) * a.N + j0 + 32 * kNY * wj + c0);
       __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
                                              rg, goff, 0, 0);
       __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])},
@@ -561,12 +595,15 @@ int cu_count() {
 }
 
 // Two stages (two workgroups per CU) when the grid fills the GPU twice over,
-// otherwise three (one workgroup per CU, two k steps in flight).
+// otherwise three (one workgroup per CU, two k steps in flight); k-major
+// products whose 128 x 128 grid would leave CUs idle take 128 x 64 tiles.
 void polar_gemm(bool tr, const PolarGemm& a, int batch, hipStream_t s, int cus) {
   const int64_t grid = (int64_t)(a.M / kGemmTile) * (a.N / kGemmTile) * batch;
   const bool deep = grid < 2 * (int64_t)cus;
   const dim3 g((unsigned)grid), b(256);
-  if (tr && deep) hipLaunchKernelGGL((polar_gemm_kernel<true, 3>), g, b, 0, s, a);
+  if (tr && grid < (int64_t)cus)
+    hipLaunchKernelGGL((polar_gemm_kernel<true, 3, true>), dim3((unsigned)(2 * grid)), b, 0, s, a);
+  else if (tr && deep) hipLaunchKernelGGL((polar_gemm_kernel<true, 3>), g, b, 0, s, a);
   else if (tr) hipLaunchKernelGGL((polar_gemm_kernel<true, 2>), g, b, 0, s, a);
   else if (deep) hipLaunchKernelGGL((polar_gemm_kernel<false, 3>), g, b, 0, s, a);
   else hipLaunchKernelGGL((polar_gemm_kernel<false, 2>), g, b, 0, s, a);

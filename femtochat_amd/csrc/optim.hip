@@ -311,24 +311,28 @@ constexpr int kGemmTile = 128, kGemmK = 64;
 // 16-byte writes by column and reads by row group)
 constexpr int kQuadPitch = 272, kQuadBytes = 64 * kQuadPitch;
 
+// Unit swizzles of LDS tile rows: 16 units (256 B) per row; 8 units read
+// along rows (i- or j-major, 16-byte reads); 8 units read across rows
+// (k-major narrow tiles, transposed reads), kUPR = -8.
 template <int kUPR>
 __device__ constexpr int gemm_swz(int r) {
-  return kUPR == 16 ? (4 * (r & 3) + ((r >> 2) & 3)) : ((r >> 1) & 7);
+  return kUPR == 16 ? (4 * (r & 3) + ((r >> 2) & 3)) : kUPR == 8 ? ((r >> 1) & 7) : 4 * ((r >> 1) & 1);
 }
 
 // Per-lane global byte offsets of one wave's share of a tile's DMA: kRows
-// rows of kUPR 16-byte units, 1 KB blocks, block b filled by wave b mod 4;
+// rows of |kUPR| 16-byte units, 1 KB blocks, block b filled by wave b mod 4;
 // lane l of block b writes physical unit 64 b + l.
-template <int kUPR>
+template <int kUPR, int kRowsT = 1024 / (kUPR < 0 ? -kUPR : kUPR)>
 struct GemmDma {
-  static constexpr int kRows = 1024 / kUPR;  // 16 KB tiles
-  static constexpr int kPer = kRows * kUPR / 64 / kWaves;
+  static constexpr int kUnits = kUPR < 0 ? -kUPR : kUPR;
+  static constexpr int kRows = kRowsT;  // 16 KB tiles by default
+  static constexpr int kPer = kRows * kUnits / 64 / kWaves;
   int goff[kPer];
   __device__ inline void init(int wave, int lane, int pitch_bytes) {
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int unit = 64 * (wave + kWaves * j) + lane;
-      const int row = unit / kUPR, pu = unit % kUPR;
+      const int row = unit / kUnits, pu = unit % kUnits;
       goff[j] = row * pitch_bytes + 16 * (pu ^ gemm_swz<kUPR>(row));
     }
   }
@@ -348,13 +352,12 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// kNarrow (with kTr, for A = X X^T when 128 x 128 tiles would not fill the
-// CUs): 128 x 64 tiles, each wave 64 x 32 (2 x 1 blocks); the Q tile is 64
-// rows of k by 64 values (128 B per row, units swizzled by 4 ((r/2) mod 2),
-// which keeps its transposed reads free of bank conflicts).
+// kNarrow (when 128 x 128 tiles would not fill the CUs): 128 x 64 tiles,
+// each wave 64 x 32 (2 x 1 blocks); the Q tile is 64 rows by 64 values (128 B
+// per row; k-major, its units are swizzled by 4 ((r/2) mod 2), which keeps
+// its transposed reads free of bank conflicts).
 template <bool kTr, int kStages, bool kNarrow = false>
 __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(PolarGemm a) {
-  static_assert(!kNarrow || kTr, "narrow tiles are for the k-major products");
   constexpr int kTN = kNarrow ? 64 : kGemmTile;  // tile width (j)
   constexpr int kNY = kTN / 64;                   // 32-column blocks per wave
   constexpr int kQBytes = kNarrow ? 8192 : 16384;
@@ -379,24 +382,8 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
   using Dma = GemmDma<kTr ? 16 : 8>;
   Dma pdma;
   pdma.init(wave, lane, 2 * a.ldp);
-  // the narrow Q tile: 8 blocks of 1 KB, two per wave, block b at 64 b + lane
-  // units, 8 units per row
-  struct NarrowDma {
-    int goff[2];
-    __device__ inline void init(int wave, int lane, int pitch_bytes) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int unit = 64 * (wave + kWaves * j) + lane, row = unit / 8, pu = unit % 8;
-        goff[j] = row * pitch_bytes + 16 * (pu ^ (4 * ((row >> 1) & 1)));
-      }
-    }
-    __device__ inline void issue(u32x4s words, int tile_off, uint32_t lds, int wave) const {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        dma_load16(words, goff[j] + tile_off, __builtin_amdgcn_readfirstlane(lds + 1024 * (wave + kWaves * j)));
-    }
-  };
-  typename std::conditional<kNarrow, NarrowDma, Dma>::type qdma;
+  using QDma = typename std::conditional<kNarrow, GemmDma<kTr ? -8 : 8, 64>, Dma>::type;
+  QDma qdma;
   qdma.init(wave, lane, 2 * a.ldq);
   // tile origin of k step s: rows 64s, columns i0 (P) or j0 (Q) when kTr,
   // else rows i0 or j0, columns 64s
@@ -420,7 +407,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
   // i- or j-major tiles: row 64 wi + 32 x + l32 (P) or 64 wj + 32 y + l32 (Q),
   // unit 2c + g (chunk c is ^ 32c)
   const int nat = l32 * 128 + 16 * (g ^ gemm_swz<8>(l32));
-  const int natp = nat + 64 * 128 * wi, natq = nat + 64 * 128 * wj;
+  const int natp = nat + 64 * 128 * wi, natq = nat + 32 * kNY * 128 * wj;
 
   f32x16 acc[2][kNY];
 #pragma unroll
@@ -449,7 +436,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
   // k steps s .. s + kStages - 2 are in flight while step s is multiplied
   // (each wave issues kDmaPer loads per step); a step's stage is refilled
   // after the barrier that follows every wave's last read of it
-  constexpr int kDmaPer = Dma::kPer + (kNarrow ? 2 : Dma::kPer);
+  constexpr int kDmaPer = Dma::kPer + QDma::kPer;
   const int steps = a.K / kGemmK;
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
@@ -476,7 +463,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
       }
 #pragma unroll
       for (int y = 0; y < kNY; ++y) {
-        if (kNarrow) {
+        if (kTr && kNarrow) {
           q[y] = lds_tr_frag(qt, trn[0] + 2048 * c, trn[1] + 2048 * c);
         } else if (kTr) {
           const int blk = 128 * wj + 64 * y;
@@ -498,7 +485,7 @@ __global__ __launch_bounds__(256, kStages == 2 ? 2 : 1) void polar_gemm_kernel(P
     }
     // keep that order through scheduling: LDS reads of chunk c + 1 ahead of
     // the products of chunk c (masks: 0x100 LDS read, 0x008 MFMA)
-    constexpr int kReads = kTr ? 4 + 2 * kNY : 4;
+    constexpr int kReads = kTr ? 4 + 2 * kNY : 2 + kNY;
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
     for (int c = 0; c < kGemmK / 16 - 1; ++c) {
@@ -595,15 +582,16 @@ int cu_count() {
 }
 
 // Two stages (two workgroups per CU) when the grid fills the GPU twice over,
-// otherwise three (one workgroup per CU, two k steps in flight); k-major
-// products whose 128 x 128 grid would leave CUs idle take 128 x 64 tiles.
+// otherwise three (one workgroup per CU, two k steps in flight); products
+// whose 128 x 128 grid would leave CUs idle take 128 x 64 tiles.
 void polar_gemm(bool tr, const PolarGemm& a, int batch, hipStream_t s, int cus) {
   const int64_t grid = (int64_t)(a.M / kGemmTile) * (a.N / kGemmTile) * batch;
   const bool deep = grid < 2 * (int64_t)cus;
   const dim3 g((unsigned)grid), b(256);
-  if (tr && grid < (int64_t)cus)
-    hipLaunchKernelGGL((polar_gemm_kernel<true, 3, true>), dim3((unsigned)(2 * grid)), b, 0, s, a);
-  else if (tr && deep) hipLaunchKernelGGL((polar_gemm_kernel<true, 3>), g, b, 0, s, a);
+  if (grid < (int64_t)cus) {
+    if (tr) hipLaunchKernelGGL((polar_gemm_kernel<true, 3, true>), dim3((unsigned)(2 * grid)), b, 0, s, a);
+    else hipLaunchKernelGGL((polar_gemm_kernel<false, 3, true>), dim3((unsigned)(2 * grid)), b, 0, s, a);
+  } else if (tr && deep) hipLaunchKernelGGL((polar_gemm_kernel<true, 3>), g, b, 0, s, a);
   else if (tr) hipLaunchKernelGGL((polar_gemm_kernel<true, 2>), g, b, 0, s, a);
   else if (deep) hipLaunchKernelGGL((polar_gemm_kernel<false, 3>), g, b, 0, s, a);
   else hipLaunchKernelGGL((polar_gemm_kernel<false, 2>), g, b, 0, s, a);

@@ -172,9 +172,12 @@ def _torch_polar_bf16(G):
     return torch.stack(out)
 
 
-# sizes that are multiples of 128 run the library's own MFMA GEMM, the others rocBLAS
+# sizes that are multiples of 128 run the library's own MFMA GEMM (128 x 64 tiles
+# for grids below the CU count), the others rocBLAS
 @pytest.mark.parametrize("m,n,k", [(64, 64, 3), (160, 48, 2), (128, 128, 3), (256, 384, 2), (384, 256, 2),
-                                   (512, 512, 4), (512, 2048, 1), (2048, 512, 1)])
+                                   (512, 512, 4), (512, 2048, 1), (2048, 512, 1),
+                                   # training sizes: grids of 128 x 128 tiles at and above the CU count
+                                   (512, 512, 16), (512, 512, 32), (2048, 512, 8)])
 def test_polar_express_bf16_compute(gpu, m, n, k):
     g = torch.Generator().manual_seed(m * 5 + n)
     G = torch.randn(k, n, m, generator=g)

@@ -272,7 +272,8 @@ __global__ __launch_bounds__(256) void copy_scaled_kernel(int R, int C, const S*
 //   else: P(i, k) at P[i ldp + k], Q(k, j) at Q[j ldq + k]  (contiguous in k)
 //   C, D  column-major M x N (leading dimension M)
 // A workgroup of four waves computes a 128 x 128 tile of D, each wave 64 x 64
-// as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16.  The k loop runs in steps of
+// as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 x 64 and 64 x 32, 2 x 1
+// blocks, for grids that would leave CUs idle).  The k loop runs in steps of
 // 64 through kStages LDS stages filled by direct global->LDS loads (two, at
 // two workgroups per CU; three, at one, when the grid leaves CUs free): the
 // next kStages - 1 steps' loads are in flight while a step's products run,

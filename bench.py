@@ -66,21 +66,28 @@ def measured_traffic(workload: str) -> dict:
 
 
 def cpu_baseline(wl, rows: int, threads: int) -> dict:
-    """Time the reference's blocked FA-1 CPU algorithm (float32 restatement in
-    oracle/fa1.c, 512-blocks, no skipping) on a bounded sample of the same
-    workload: ``rows`` batch rows, all heads, bf16 inputs upcast to fp32."""
+    """Time the reference's blocked CPU attention (oracle/fa1_blas.py: the
+    loop nest and 512-wide blocks of flash_attention₁!/Δflash_attention₁!,
+    src/kernels.jl:131-379, no block skipping, every product a BLAS sgemm as
+    the reference's mul! calls) on a bounded sample of the same workload:
+    ``rows`` batch rows, all heads, bf16-rounded inputs in float32 (the
+    reference's CPU path computes in the input type; its BFloat16 matmul is a
+    generic fallback, so the fp32 path is the one to time)."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
 
     from femtochat_amd import workloads as W
-    from oracle import fa1
+    from oracle import fa1_blas
 
     h = W.host_inputs(wl, 0, batch=list(range(rows)))
-    fa1.forward(h.Q[:, :64], h.K[:, :64], h.V[:, :64], h.window, nthreads=threads)  # warm-up (loads, pages)
-    t0 = time.perf_counter()
-    O, l, m = fa1.forward(h.Q, h.K, h.V, h.window, h.positions, nthreads=threads)
-    t1 = time.perf_counter()
-    fa1.backward(h.dO, h.Q, h.K, h.V, O, l, m, h.window, h.positions, nthreads=threads)
-    t2 = time.perf_counter()
+    with threadpool_limits(limits=threads, user_api="blas"):
+        blas = fa1_blas.blas_info()
+        fa1_blas.forward(h.Q[:1, :512], h.K[:1, :512], h.V[:1, :512], h.window)  # warm-up (pages, threads)
+        t0 = time.perf_counter()
+        O, l, m = fa1_blas.forward(h.Q, h.K, h.V, h.window, h.positions)
+        t1 = time.perf_counter()
+        fa1_blas.backward(h.dO, h.Q, h.K, h.V, O, l, m, h.window, h.positions)
+        t2 = time.perf_counter()
     pairs = W.visible_pairs(wl.T, rows, wl.H, h.window, h.positions)
     flop = 14 * wl.D * pairs
     assert np.isfinite(O).all()
@@ -89,10 +96,15 @@ def cpu_baseline(wl, rows: int, threads: int) -> dict:
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
+        "blas": blas,
+        "fwd_s": round(t1 - t0, 3),
+        "bwd_s": round(t2 - t1, 3),
         "sample": (f"{wl.name} batch rows 0..{rows - 1} of {wl.B}, all {wl.H} heads, T={wl.T}: fwd {t1 - t0:.2f} s "
-                   f"+ bwd {t2 - t1:.2f} s; float32 restatement of flash_attention₁!/Δflash_attention₁! "
-                   "(src/kernels.jl:131-379, 512-blocks, no tile skipping) on bf16-rounded inputs upcast to fp32; "
-                   "TFLOP/s counts algorithmic visible-pair FLOPs like the GPU value"),
+                   f"+ bwd {t2 - t1:.2f} s; the reference's blocked algorithm (flash_attention₁!/Δflash_attention₁!, "
+                   "src/kernels.jl:131-379: 512-blocks, no skipping, products as BLAS sgemm) in float32 on "
+                   f"bf16-rounded inputs, {blas.get('library', 'BLAS')} {blas.get('version', '')} with "
+                   f"{blas.get('threads', threads)} threads (the Python loop itself single-threaded, as the "
+                   "reference's Julia loop); TFLOP/s counts algorithmic visible-pair FLOPs like the GPU value"),
     }
 
 
@@ -313,35 +325,18 @@ def _hbm_roofline(nbytes: int, ms: float) -> dict:
             "frac": round(achieved / PEAK_HBM_GBS, 4)}
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="C3")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-rows", type=int, default=16, help="batch rows in the CPU baseline sample")
-    ap.add_argument("--sections", default="prologue,loss,optim",
-                    help="measurements besides the headline attention step (comma list of prologue, loss, optim; "
-                         "'none' for only the headline)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: every box in this build has a single MI355X, and the attention "
-              f"kernels need no collective (--gpus {args.gpus} is not supported).", file=sys.stderr)
-        return 2
-
+def measure_attention(wl, dev, steps: int, warmup: int) -> dict:
+    """One fwd+bwd step (every layer of the workload, overwrite) timed over
+    ``steps`` after ``warmup``, with per-kernel times from the library's HIP
+    events on the launch stream."""
     import torch
 
     import femtochat_amd._lib as L
     from femtochat_amd import MFMAExact, MFMAFast, attention_, backward_workspace_bytes, delta_attention_
     from femtochat_amd import workloads as W
 
-    wl = W.WORKLOADS[args.workload]
-    dev = torch.device("cuda", 0)
     fast = wl.mode == "fast"
     A = MFMAFast() if fast else MFMAExact()
-    dt = torch.bfloat16 if fast else torch.float32
-
     layers = []
     total_pairs = 0
     for layer in range(wl.layers):
@@ -353,41 +348,78 @@ def main() -> int:
         ws = torch.empty(backward_workspace_bytes(A, Q, K, positions=pos), dtype=torch.uint8, device=dev)
         pairs = W.visible_pairs(wl.T, wl.B, wl.H, window, None if pos is None else pos.cpu().numpy())
         total_pairs += pairs
-        layers.append((Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws, pairs))
+        layers.append((Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws))
 
     def step():
-        for (Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws, _) in layers:
+        for (Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws) in layers:
             attention_(A, O, l, m, Q, K, V, window, positions=pos)
             delta_attention_(A, dQ, dK, dV, dO, Q, K, V, O, l, m, window, positions=pos, accumulate=False,
                              workspace=ws)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     L.profile_collect()  # discard anything recorded before
     L.profile_enable(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     L.profile_enable(False)
     kernels = L.profile_collect()
 
-    ms = (t1 - t0) * 1e3 / args.steps
+    ms = (t1 - t0) * 1e3 / steps
     flop = 14 * wl.D * total_pairs
     value = flop / (ms * 1e-3) / 1e12
     peak = PEAK_BF16_TFLOPS if fast else PEAK_FP32_TFLOPS
-
     per_kernel = {}
     for name, (n, tot) in sorted(kernels.items()):
         avg = tot / n
         bound, amount, unit = kernel_flops(name, wl.D, total_pairs // wl.layers, wl.B, wl.T, wl.H)
         rate = amount / (avg * 1e-3)
-        per_kernel[name] = {"launches": n, "avg_ms": round(avg, 4), "bound": bound,
-                            "achieved": round(rate / (1e12 if unit == "flop" else 1e9), 2),
-                            "unit": "TFLOP/s" if unit == "flop" else "GB/s"}
+        kpeak = peak if bound == "mfma" else PEAK_HBM_GBS
+        achieved = rate / (1e12 if unit == "flop" else 1e9)
+        per_kernel[name] = {"launches": n, "avg_ms": round(avg, 4), "bound": bound, "achieved": round(achieved, 2),
+                            "unit": "TFLOP/s" if unit == "flop" else "GB/s", "frac": round(achieved / kpeak, 4)}
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": f"{wl.name}: {wl.description}", "mode": wl.mode, "layers": wl.layers,
+            "ms_per_step": round(ms, 4), "tflops": round(value, 2), "peak_tflops": peak,
+            "peak_frac": round(value / peak, 4), "visible_pairs": total_pairs, "flop_per_step": flop,
+            "steps": steps, "kernels": per_kernel, "raw": kernels}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="C3")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=16, help="batch rows in the CPU baseline sample")
+    ap.add_argument("--configs", default="C1,C2,C4,C5",
+                    help="other BASELINE workloads timed beside the headline (comma list; '' for none)")
+    ap.add_argument("--sections", default="prologue,loss,optim",
+                    help="measurements besides the headline attention step (comma list of prologue, loss, optim; "
+                         "'none' for only the headline)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box in this build has a single MI355X, and the attention "
+              f"kernels need no collective (--gpus {args.gpus} is not supported).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from femtochat_amd import workloads as W
+
+    wl = W.WORKLOADS[args.workload]
+    dev = torch.device("cuda", 0)
+    fast = wl.mode == "fast"
+    head = measure_attention(wl, dev, args.steps, args.warmup)
+    ms, flop, value, peak = head["ms_per_step"], head["flop_per_step"], head["tflops"], head["peak_tflops"]
+    total_pairs, per_kernel, kernels = head["visible_pairs"], head["kernels"], head["raw"]
     dominant = max(kernels.items(), key=lambda kv: kv[1][1])[0]
     dk = per_kernel[dominant]
     dpeak = peak if dk["bound"] == "mfma" else PEAK_HBM_GBS
@@ -401,6 +433,14 @@ def main() -> int:
         if key:
             rec["hbm_bytes"] = traffic[key]
             rec["hbm_gbs"] = round(traffic[key] / (rec["avg_ms"] * 1e-3) / 1e9, 1)
+
+    # The other BASELINE configurations, each a full step (all its layers):
+    # parity cases in tests/, timed here beside the headline.
+    configs = {}
+    for name in [c for c in args.configs.split(",") if c and c != wl.name]:
+        r = measure_attention(W.WORKLOADS[name], dev, max(3, args.steps // 2), max(2, args.warmup // 2))
+        r.pop("raw")
+        configs[name] = r
 
     sections = set(args.sections.split(",")) if fast else set()
     prologue = measure_prologue(wl, dev, args.steps) if "prologue" in sections else None
@@ -435,6 +475,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": per_kernel,
+        "configs": configs,
         "prologue": prologue,
         "loss": loss_side,
         "optim": optim_side,

@@ -21,7 +21,9 @@ from .kernels import (  # noqa: F401
     attention_state,
     backward_workspace_bytes,
     capabilities,
+    convert_,
     delta_attention_,
+    fill_zero_,
     instruction,
     window_sizes,
 )

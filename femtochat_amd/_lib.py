@@ -197,6 +197,8 @@ _SIGNATURES = {
     "fc_polar_express": (ctypes.c_int, [ctypes.POINTER(PolarDesc), _P, _P, ctypes.c_size_t, _P]),
     "fc_polar_express_grouped": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(PolarDesc), ctypes.POINTER(_P),
                                                 ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_size_t), _P]),
+    "fc_convert": (ctypes.c_int, [_P, ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_int64, _P]),
+    "fc_fill_zero": (ctypes.c_int, [_P, ctypes.c_size_t, _P]),
     "fc_capabilities": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(Caps)]),
     "fc_profile_enable": (ctypes.c_int, [ctypes.c_int32]),
     "fc_profile_collect": (

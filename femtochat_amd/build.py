@@ -15,7 +15,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
-SOURCES = ["attn_api.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_fwd_fast.hip", "attn_bwd_fast.hip", "rope_norm.hip", "loss.hip", "xla_bridge.hip", "optim.hip", "embed_sort.hip"]
+SOURCES = ["attn_api.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_fwd_fast.hip", "attn_bwd_fast.hip", "rope_norm.hip", "loss.hip", "xla_bridge.hip", "optim.hip", "embed_sort.hip", "convert.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -54,56 +54,13 @@ void clear_error() { g_last_error.clear(); }
 
 namespace {
 
-bool valid_dtype(int32_t d) { return d == FC_F32 || d == FC_BF16; }
+using fc::valid_dtype;
 
-// Validates the descriptor and fills the normalised problem.
+// Validates the descriptor and fills the normalised problem (attn_problem.hpp).
 fc_status make_problem(const fc_attn_desc* d, fc::Problem* p) {
-  if (d == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "descriptor is null");
-  if (d->D <= 0 || d->H <= 0 || d->Hkv <= 0 || d->T <= 0 || d->B <= 0)
-    return fail(FC_ERR_INVALID_ARGUMENT, "sizes must be positive (D=%d H=%d Hkv=%d T=%d B=%d)", d->D, d->H,
-                d->Hkv, d->T, d->B);
-  if (d->H % d->Hkv != 0)
-    return fail(FC_ERR_INVALID_ARGUMENT, "n_head %d is not a multiple of n_kv_head %d", d->H, d->Hkv);
-  if (d->D % 16 != 0 || d->D > 128)
-    return fail(FC_ERR_INVALID_ARGUMENT, "head_dim %d must be a multiple of 16 and at most 128", d->D);
-  if (!fc::head_dim_supported(d->D))
-    return fail(FC_ERR_UNSUPPORTED, "head_dim %d is not compiled in (supported: 16, 32, 64, 128)", d->D);
-  const int64_t rows = (int64_t)d->B * d->T * d->H;
-  if (rows * d->D >= (int64_t)1 << 40 || (int64_t)d->T * d->H * d->B > INT32_MAX / 2)
-    return fail(FC_ERR_UNSUPPORTED, "problem too large");
-  if (!valid_dtype(d->in_dtype) || !valid_dtype(d->out_dtype) || !valid_dtype(d->dout_dtype) ||
-      !valid_dtype(d->grad_dtype))
-    return fail(FC_ERR_INVALID_ARGUMENT, "dtype codes must be FC_F32 or FC_BF16");
-  if (d->mode == FC_MODE_EXACT) {
-    if (d->in_dtype != FC_F32 || d->out_dtype != FC_F32 || d->dout_dtype != FC_F32 || d->grad_dtype != FC_F32)
-      return fail(FC_ERR_INVALID_ARGUMENT, "exact mode takes and returns float32 only");
-  } else if (d->mode == FC_MODE_FAST) {
-    if (d->in_dtype != FC_BF16)
-      return fail(FC_ERR_INVALID_ARGUMENT, "fast mode takes bfloat16 Q/K/V (convert first, as attention_inputs does)");
-  } else {
-    return fail(FC_ERR_INVALID_ARGUMENT, "unknown mode %d", d->mode);
-  }
-  if ((d->flags & ~FC_FLAG_OVERWRITE) != 0) return fail(FC_ERR_INVALID_ARGUMENT, "unknown flag bits 0x%x", d->flags);
-
-  p->D = d->D;
-  p->H = d->H;
-  p->Hkv = d->Hkv;
-  p->T = d->T;
-  p->B = d->B;
-  p->group = d->H / d->Hkv;
-  int64_t left = d->win_left, right = d->win_right;
-  if (left == -1 && right == 0) left = d->T;  // causal sentinel (src/kernels.jl:35-36)
-  // Clamping to [-T-1, T] keeps q - left and q + right in range without
-  // changing which keys of [0, T) are visible.
-  const int64_t lo = -(int64_t)d->T - 1, hi = d->T;
-  p->left = (int)std::min(std::max(left, lo), hi);
-  p->right = (int)std::min(std::max(right, lo), hi);
-  p->bf16 = d->mode == FC_MODE_FAST;
-  p->out_bf16 = d->out_dtype == FC_BF16;
-  p->dout_bf16 = d->dout_dtype == FC_BF16;
-  p->grad_bf16 = d->grad_dtype == FC_BF16;
-  p->accumulate = (d->flags & FC_FLAG_OVERWRITE) == 0;
-  p->positions = false;
+  char msg[256];
+  const fc_status st = fc::make_problem(d, p, msg, sizeof(msg));
+  if (st != FC_OK) return fail(st, "%s", msg);
   return FC_OK;
 }
 

@@ -494,22 +494,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dq_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-BwdWorkspace bwd_workspace(const Problem& p) {
-  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
-  BwdWorkspace w{};
-  const size_t nq = (size_t)p.B * p.H * p.T;
-  size_t off = 0;
-  w.delta = off;
-  off = align(off + nq * sizeof(float));
-  w.lse2 = off;
-  off = align(off + nq * sizeof(float));
-  w.chunk_lb = off;
-  if (p.positions) off = align(off + (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t));
-  w.dO16 = off;
-  if (p.bf16 && !p.dout_bf16) off = align(off + nq * p.D * sizeof(uint16_t));
-  w.total = off;
-  return w;
-}
 
 template <int D, typename TO, typename TD>
 static hipError_t launch_pre_t(const Problem& p, const PreArgs& a, hipStream_t s) {

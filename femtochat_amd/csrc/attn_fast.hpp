@@ -187,18 +187,44 @@ __device__ inline void dma_load16(u32x4s words, int voff, uint32_t lds_addr) {
       : "memory", "m0");
 }
 
-template <int D, int R>
+// The same for 4 bytes per lane (a 256-byte block of LDS).
+__device__ inline void dma_load4(u32x4s words, int voff, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "buffer_load_dword %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(words), "s"(lds_addr)
+      : "memory", "m0");
+}
+
+// Waits until at most n of this wave's global loads (LDS-DMA included) are
+// outstanding; loads complete in issue order, so the older ones have landed.
+__device__ inline void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+  }
+}
+
+template <int D, int R, int NW = kWaves>
 struct DmaPlan {
   using Tile = SwzTile<D>;
   static constexpr int kInstr = R * Tile::kUPR / 64;  // 1 KB blocks per tile
   static_assert(R * Tile::kUPR % 64 == 0, "tile must be a whole number of 1 KB blocks");
-  static constexpr int kPerWave = (kInstr + kWaves - 1) / kWaves;
+  static constexpr int kPerWave = (kInstr + NW - 1) / NW;
   int goff[kPerWave];
 
   __device__ inline void init(int wave, int lane, int pitch_bytes) {
 #pragma unroll
     for (int j = 0; j < kPerWave; ++j) {
-      const int i = wave + kWaves * j;
+      const int i = wave + NW * j;
       const int P = 64 * i + lane;
       const int row = P / Tile::kUPR, pu = P % Tile::kUPR;
       goff[j] = row * pitch_bytes + 16 * (pu ^ Tile::swz(row));
@@ -212,9 +238,15 @@ struct DmaPlan {
   // The j-th of them, for callers that spread the loads over their compute;
   // j >= kPerWave issues nothing.
   __device__ inline void issue_one(u32x4s words, uint32_t lds_addr, int wave, int j) const {
-    const int i = wave + kWaves * j;
-    if (j < kPerWave && (kInstr % kWaves == 0 || i < kInstr))
+    const int i = wave + NW * j;
+    if (j < kPerWave && (kInstr % NW == 0 || i < kInstr))
       dma_load16(words, goff[j], __builtin_amdgcn_readfirstlane(lds_addr + 1024 * i));
+  }
+  // Number of loads issue() makes on wave `wave`.
+  __host__ __device__ static constexpr int count(int wave) {
+    int n = 0;
+    for (int j = 0; j < kPerWave; ++j) n += (wave + NW * j < kInstr) ? 1 : 0;
+    return n;
   }
 };
 

@@ -238,6 +238,5 @@ hipError_t launch_fwd(const Problem& p, const FwdArgs& a, hipStream_t s) {
   return p.bf16 ? launch_fwd_fast(p, a, s) : launch_fwd_e<float>(p, a, s);
 }
 
-bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 }  // namespace fc

@@ -5,23 +5,11 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/femtochat_attn.h"
+#include "attn_problem.hpp"
 #include <stddef.h>
 #include <stdint.h>
 
 namespace fc {
-
-// Normalised problem: window already mapped to (left,right) with the causal
-// sentinel (-1,0) replaced by (T,0) and both extents clamped to [-T-1, T].
-struct Problem {
-  int D, H, Hkv, T, B, group;
-  int left, right;
-  bool bf16;        // fast mode (bf16 inputs) vs exact mode (fp32)
-  bool out_bf16;    // O storage
-  bool dout_bf16;   // dO storage
-  bool grad_bf16;   // dQ/dK/dV storage
-  bool accumulate;  // backward adds into dQ/dK/dV
-  bool positions;
-};
 
 struct FwdArgs {
   const void* Q;
@@ -161,14 +149,6 @@ struct EmbedSortLayout {
 };
 EmbedSortLayout embed_sort_layout(int64_t N, int vocab);
 hipError_t launch_embed_sorted(const EmbedArgs& a, bool bf16_dy, void* workspace, hipStream_t s);
-
-// Workspace layout of the backward pass (byte offsets, 256-aligned).
-struct BwdWorkspace {
-  size_t delta, lse2, chunk_lb, dO16, total;
-};
-BwdWorkspace bwd_workspace(const Problem& p);
-
-bool head_dim_supported(int D);
 
 // Kernel launchers (return the hipError_t of the launch).
 hipError_t launch_fwd(const Problem& p, const FwdArgs& a, hipStream_t s);

@@ -1,0 +1,136 @@
+// Host-side problem description of the attention entry points: descriptor
+// validation, the normalised window and the backward workspace layout.
+// Plain C++ (no HIP), so a host-only harness can build and check it alone.
+#pragma once
+
+#include "../../include/femtochat_attn.h"
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <algorithm>
+
+namespace fc {
+
+// Normalised problem: window already mapped to (left,right) with the causal
+// sentinel (-1,0) replaced by (T,0) and both extents clamped to [-T-1, T].
+struct Problem {
+  int D, H, Hkv, T, B, group;
+  int left, right;
+  bool bf16;        // fast mode (bf16 inputs) vs exact mode (fp32)
+  bool out_bf16;    // O storage
+  bool dout_bf16;   // dO storage
+  bool grad_bf16;   // dQ/dK/dV storage
+  bool accumulate;  // backward adds into dQ/dK/dV
+  bool positions;
+};
+
+// Head dims the kernels are compiled for.
+inline bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+
+inline bool valid_dtype(int32_t d) { return d == FC_F32 || d == FC_BF16; }
+
+// Largest byte extent of one (batch, head) slice that the fast-mode kernels
+// address with 32-bit buffer offsets: the last row's start plus one row.
+inline int64_t fast_slice_bytes(int T, int heads, int D) { return (int64_t)(T - 1) * heads * D * 2 + 2 * D; }
+
+// Validates the descriptor and fills the normalised problem; on failure
+// writes a message into msg (msg_len bytes) and returns the status.
+inline fc_status make_problem(const fc_attn_desc* d, Problem* p, char* msg, size_t msg_len) {
+  auto bad = [&](fc_status code, const char* text) {
+    snprintf(msg, msg_len, "%s", text);
+    return code;
+  };
+  if (d == nullptr) return bad(FC_ERR_INVALID_ARGUMENT, "descriptor is null");
+  if (d->D <= 0 || d->H <= 0 || d->Hkv <= 0 || d->T <= 0 || d->B <= 0) {
+    snprintf(msg, msg_len, "sizes must be positive (D=%d H=%d Hkv=%d T=%d B=%d)", d->D, d->H, d->Hkv, d->T, d->B);
+    return FC_ERR_INVALID_ARGUMENT;
+  }
+  if (d->H % d->Hkv != 0) {
+    snprintf(msg, msg_len, "n_head %d is not a multiple of n_kv_head %d", d->H, d->Hkv);
+    return FC_ERR_INVALID_ARGUMENT;
+  }
+  if (d->D % 16 != 0 || d->D > 128) {
+    snprintf(msg, msg_len, "head_dim %d must be a multiple of 16 and at most 128", d->D);
+    return FC_ERR_INVALID_ARGUMENT;
+  }
+  if (!head_dim_supported(d->D)) {
+    snprintf(msg, msg_len, "head_dim %d is not compiled in (supported: 16, 32, 64, 128)", d->D);
+    return FC_ERR_UNSUPPORTED;
+  }
+  const int64_t rows = (int64_t)d->B * d->T * d->H;
+  if (rows * d->D >= (int64_t)1 << 40 || rows > INT32_MAX / 2) return bad(FC_ERR_UNSUPPORTED, "problem too large");
+  if (!valid_dtype(d->in_dtype) || !valid_dtype(d->out_dtype) || !valid_dtype(d->dout_dtype) ||
+      !valid_dtype(d->grad_dtype))
+    return bad(FC_ERR_INVALID_ARGUMENT, "dtype codes must be FC_F32 or FC_BF16");
+  if (d->mode == FC_MODE_EXACT) {
+    if (d->in_dtype != FC_F32 || d->out_dtype != FC_F32 || d->dout_dtype != FC_F32 || d->grad_dtype != FC_F32)
+      return bad(FC_ERR_INVALID_ARGUMENT, "exact mode takes and returns float32 only");
+  } else if (d->mode == FC_MODE_FAST) {
+    if (d->in_dtype != FC_BF16)
+      return bad(FC_ERR_INVALID_ARGUMENT, "fast mode takes bfloat16 Q/K/V (convert first, as attention_inputs does)");
+    // The fast kernels read a (batch, head) slice through one buffer
+    // descriptor with 32-bit offsets.
+    if (fast_slice_bytes(d->T, d->H, d->D) >= ((int64_t)1 << 31) ||
+        fast_slice_bytes(d->T, d->Hkv, d->D) >= ((int64_t)1 << 31)) {
+      snprintf(msg, msg_len, "fast mode: a (batch, head) slice of T*H*D = %lld bf16 values spans 2^31 bytes or more",
+               (long long)d->T * d->H * d->D);
+      return FC_ERR_UNSUPPORTED;
+    }
+  } else {
+    snprintf(msg, msg_len, "unknown mode %d", d->mode);
+    return FC_ERR_INVALID_ARGUMENT;
+  }
+  if ((d->flags & ~FC_FLAG_OVERWRITE) != 0) {
+    snprintf(msg, msg_len, "unknown flag bits 0x%x", d->flags);
+    return FC_ERR_INVALID_ARGUMENT;
+  }
+
+  p->D = d->D;
+  p->H = d->H;
+  p->Hkv = d->Hkv;
+  p->T = d->T;
+  p->B = d->B;
+  p->group = d->H / d->Hkv;
+  int64_t left = d->win_left, right = d->win_right;
+  if (left == -1 && right == 0) left = d->T;  // causal sentinel (src/kernels.jl:35-36)
+  // Clamping to [-T-1, T] keeps q - left and q + right in range without
+  // changing which keys of [0, T) are visible.
+  const int64_t lo = -(int64_t)d->T - 1, hi = d->T;
+  p->left = (int)std::min(std::max(left, lo), hi);
+  p->right = (int)std::min(std::max(right, lo), hi);
+  p->bf16 = d->mode == FC_MODE_FAST;
+  p->out_bf16 = d->out_dtype == FC_BF16;
+  p->dout_bf16 = d->dout_dtype == FC_BF16;
+  p->grad_bf16 = d->grad_dtype == FC_BF16;
+  p->accumulate = (d->flags & FC_FLAG_OVERWRITE) == 0;
+  p->positions = false;
+  return FC_OK;
+}
+
+// Workspace layout of the backward pass (byte offsets, 256-aligned): Delta
+// and the base-2 log-sum-exp per query, per-32-query key bounds with
+// positions, and a bf16 copy of an fp32 dO in fast mode.
+struct BwdWorkspace {
+  size_t delta, lse2, chunk_lb, dO16, total;
+};
+
+inline BwdWorkspace bwd_workspace(const Problem& p) {
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  BwdWorkspace w{};
+  const size_t nq = (size_t)p.B * p.H * p.T;
+  size_t off = 0;
+  w.delta = off;
+  off = align(off + nq * sizeof(float));
+  w.lse2 = off;
+  off = align(off + nq * sizeof(float));
+  w.chunk_lb = off;
+  if (p.positions) off = align(off + (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t));
+  w.dO16 = off;
+  if (p.bf16 && !p.dout_bf16) off = align(off + nq * p.D * sizeof(uint16_t));
+  w.total = off;
+  return w;
+}
+
+}  // namespace fc

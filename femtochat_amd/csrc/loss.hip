@@ -365,7 +365,11 @@ hipError_t launch_xent_fused(const XentArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   profile_end(mk, "xent_fused", s);
   if (e != hipSuccess || (a.reduced == nullptr)) return e;
-  hipLaunchKernelGGL(xent_reduce_kernel, dim3(1), dim3(1024), 0, s, a);
+  // count is the caller's input here (it scaled the gradient): the reduction
+  // writes only the loss sum or mean.
+  XentArgs r = a;
+  r.count = nullptr;
+  hipLaunchKernelGGL(xent_reduce_kernel, dim3(1), dim3(1024), 0, s, r);
   return hipGetLastError();
 }
 

@@ -806,11 +806,9 @@ fc_status fc_polar_workspace_bytes(const fc_polar_desc* d, size_t* bytes) {
   return FC_OK;
 }
 
-// Polar Express of one stack on stream s with the rocBLAS handle h (held by
-// the caller under g_blas_mutex).
-static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, hipStream_t s,
-                           rocblas_handle h) {
-  fc_status st = polar_check(d);
+// Host-side checks of one stack's call (nothing is launched).
+static fc_status polar_args(const fc_polar_desc* d, const float* G, const void* workspace, size_t workspace_bytes) {
+  const fc_status st = polar_check(d);
   if (st != FC_OK) return st;
   if (G == nullptr) return failf(FC_ERR_INVALID_ARGUMENT, "polar express: G is null");
   const PolarLayout L = polar_layout(*d);
@@ -818,6 +816,16 @@ static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, si
     return failf(FC_ERR_WORKSPACE, "polar express needs %zu workspace bytes, got %zu", L.total, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
     return failf(FC_ERR_WORKSPACE, "polar express: workspace must be 256-byte aligned");
+  return FC_OK;
+}
+
+// Polar Express of one stack on stream s with the rocBLAS handle h (held by
+// the caller under g_blas_mutex).
+static fc_status polar_run(const fc_polar_desc* d, float* G, void* workspace, size_t workspace_bytes, hipStream_t s,
+                           rocblas_handle h) {
+  fc_status st = polar_args(d, G, workspace, workspace_bytes);
+  if (st != FC_OK) return st;
+  const PolarLayout L = polar_layout(*d);
   char* ws = static_cast<char*>(workspace);
   char* X = ws + L.X;
   char* Y = ws + L.Y;
@@ -916,8 +924,10 @@ fc_status fc_polar_express_grouped(int32_t count, const fc_polar_desc* descs, fl
                                    const size_t* workspace_bytes, void* stream) {
   if (count <= 0 || descs == nullptr || G == nullptr || workspaces == nullptr || workspace_bytes == nullptr)
     return failf(FC_ERR_INVALID_ARGUMENT, "polar express grouped: count must be positive and the arrays non-null");
+  // Every stack is checked before anything is launched, so a rejected call
+  // leaves no work behind on the helper streams.
   for (int i = 0; i < count; ++i) {
-    const fc_status st = polar_check(&descs[i]);
+    const fc_status st = polar_args(&descs[i], G[i], workspaces[i], workspace_bytes[i]);
     if (st != FC_OK) return st;
   }
   int dev = 0;
@@ -931,18 +941,20 @@ fc_status fc_polar_express_grouped(int32_t count, const fc_polar_desc* descs, fl
   const int used = std::min<int>(count, kHelpers);
   for (int j = 0; j < used; ++j)
     if (hipStreamWaitEvent(f->stream[j], f->start, 0) != hipSuccess) return failf(FC_ERR_HIP, "hipStreamWaitEvent failed");
-  for (int i = 0; i < count; ++i) {
+  fc_status first = FC_OK;
+  for (int i = 0; i < count && first == FC_OK; ++i) {
     const int j = i % kHelpers;
-    const fc_status st = polar_run(&descs[i], G[i], workspaces[i], workspace_bytes[i], f->stream[j], f->blas[j]);
-    if (st != FC_OK) return st;
+    first = polar_run(&descs[i], G[i], workspaces[i], workspace_bytes[i], f->stream[j], f->blas[j]);
   }
-  // join: the caller's stream waits for every helper stream
+  // join, also after a failed launch: the caller's stream waits for every
+  // helper stream, so nothing enqueued there outlives the caller's view
   for (int j = 0; j < used; ++j) {
-    if (hipEventRecord(f->done[j], f->stream[j]) != hipSuccess || hipStreamWaitEvent(s, f->done[j], 0) != hipSuccess)
-      return failf(FC_ERR_HIP, "polar express grouped: join failed");
+    if ((hipEventRecord(f->done[j], f->stream[j]) != hipSuccess || hipStreamWaitEvent(s, f->done[j], 0) != hipSuccess) &&
+        first == FC_OK)
+      first = failf(FC_ERR_HIP, "polar express grouped: join failed");
   }
-  clear_error();
-  return FC_OK;
+  if (first == FC_OK) clear_error();
+  return first;
 }
 
 }  // extern "C"

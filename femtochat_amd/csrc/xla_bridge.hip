@@ -71,7 +71,12 @@ bool run(const Slot& s, void* stream, void** b) {
     }
     case kAttnBwd: {
       const int o = s.positions ? 8 : 7;
-      void* ws = s.ws_bytes > 0 ? b[o + 3] : nullptr;
+      // XLA aligns the buffers it allocates to 64 bytes; the workspace output
+      // is declared 255 bytes longer than the library needs and used from its
+      // first 256-byte boundary.
+      void* ws = nullptr;
+      if (s.ws_bytes > 0 && b[o + 3] != nullptr)
+        ws = reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(b[o + 3]) + 255) & ~uintptr_t(255));
       return report(fc_attn_bwd(&s.attn, b[0], b[1], b[2], b[3], b[4], static_cast<const float*>(b[5]),
                                 static_cast<const float*>(b[6]),
                                 s.positions ? static_cast<const int32_t*>(b[7]) : nullptr, b[o], b[o + 1], b[o + 2],
@@ -158,7 +163,8 @@ fc_xla_callback fc_xla_bind_attention_bwd(const fc_attn_desc* desc, int32_t has_
   s.attn.flags |= FC_FLAG_OVERWRITE;  // the compiled backward writes its gradients (accumulate=false)
   if (!report(fc_attn_workspace_bytes(&s.attn, FC_PASS_BACKWARD, s.positions, &s.ws_bytes), "bind attention backward"))
     return nullptr;
-  *workspace_bytes = s.ws_bytes;
+  // Room to round the buffer XLA hands over (64-byte aligned) up to 256 bytes.
+  *workspace_bytes = s.ws_bytes > 0 ? s.ws_bytes + 255 : 0;
   return bind(s);
 }
 

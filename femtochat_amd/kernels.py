@@ -114,11 +114,13 @@ class AttentionState(NamedTuple):
 
 def window_sizes(sequence_len: int, n_layer: int, window_pattern: str = "L"):
     """Per-layer ``(left, 0)`` windows: 'S' -> ``(min(L, cld(L, 512)*128), 0)``,
-    'L' -> ``(L, 0)``, last layer forced to ``(L, 0)`` (src/parameters.jl:200-210)."""
+    any other character -> ``(L, 0)``, last layer forced to ``(L, 0)``
+    (src/parameters.jl:200-210, which tests ``== 'S'`` only).  An empty
+    pattern or no layers is an error there too (``mod1(i, 0)``, ``windows[end]``)."""
     if n_layer <= 0:
         raise ValueError("n_layer must be positive")
-    if not window_pattern or any(c not in "SL" for c in window_pattern):
-        raise ValueError(f"window_pattern must be a non-empty string of 'S' and 'L', got {window_pattern!r}")
+    if not window_pattern:
+        raise ValueError("window_pattern must not be empty")
     L = int(sequence_len)
     S = min(L, -(-L // 512) * 128)
     windows = [(S, 0) if window_pattern[i % len(window_pattern)] == "S" else (L, 0) for i in range(n_layer)]
@@ -156,16 +158,48 @@ def accumulator_type(A, dtype: torch.dtype) -> torch.dtype:
     return dtype
 
 
+def convert_(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """dst := src converted by the library (``fc_convert``): float32 and
+    bfloat16 in either direction, round to nearest even; both contiguous on
+    one GPU with the same number of elements."""
+    for name, t in (("dst", dst), ("src", src)):
+        if t.dtype not in (torch.float32, torch.bfloat16) or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 or bfloat16 GPU tensor")
+    if dst.numel() != src.numel() or dst.device != src.device:
+        raise ValueError("dst and src must have the same number of elements on the same device")
+    _lib.check(_lib.lib().fc_convert(_ptr(src), _dtype_code(src.dtype), _ptr(dst), _dtype_code(dst.dtype),
+                                     src.numel(), _stream_ptr(src.device)))
+
+
+def fill_zero_(t: torch.Tensor) -> torch.Tensor:
+    """t := 0 by the library's fill kernel (``fc_fill_zero``)."""
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("fill_zero_ needs a contiguous GPU tensor")
+    _lib.check(_lib.lib().fc_fill_zero(_ptr(t), t.numel() * t.element_size(), _stream_ptr(t.device)))
+    return t
+
+
 def attention_inputs(A, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor):
     """Precision conversion before the forward (ext/FemtoChatCUDAExt.jl:229-230):
-    the fast path stores Q/K/V in bfloat16, the exact path in float32."""
+    the fast path stores Q/K/V in bfloat16, the exact path in float32.  GPU
+    tensors are converted by the library (``fc_convert``)."""
     if isinstance(A, MFMAFast):
         target = torch.bfloat16
     elif isinstance(A, MFMAExact):
         target = torch.float32
     else:
         return Q, K, V
-    return tuple(x if x.dtype == target else x.to(target) for x in (Q, K, V))
+
+    def conv(x):
+        if x.dtype == target:
+            return x
+        if x.is_cuda and x.dtype in (torch.float32, torch.bfloat16):
+            y = torch.empty(x.shape, dtype=target, device=x.device)
+            convert_(y, x.contiguous())
+            return y
+        return x.to(target)
+
+    return tuple(conv(x) for x in (Q, K, V))
 
 
 def _stream_ptr(device: torch.device) -> ctypes.c_void_p:

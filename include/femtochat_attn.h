@@ -146,6 +146,22 @@ fc_status fc_rope_norm_bwd(const fc_rope_norm_desc* desc, const void* dY,
                            const float* cos_table, const int32_t* positions,
                            void* dX, void* stream);
 
+/* ---- Conversions the host binding needs ----------------------------------
+ * dst[i] = src[i] for 0 <= i < n, converted: float32 -> bfloat16 rounds to
+ * nearest even (NaN stays NaN, +-Inf stays +-Inf), bfloat16 -> float32 is
+ * exact, equal dtypes copy.  Replaces the conversion attention_inputs makes
+ * for the tensor-core path (reference ext/FemtoChatCUDAExt.jl:229-230, there
+ * to Float16) and the Float32.(x) of a bf16 result, so a binding converts
+ * without GPU code of its own.  Pointers must be aligned to their element
+ * size; the source and destination must not overlap unless equal. */
+fc_status fc_convert(const void* src, int32_t src_dtype, void* dst,
+                     int32_t dst_dtype, int64_t n, void* stream);
+
+/* bytes bytes of dst set to zero by a kernel (not a memset, so a captured
+   graph replays it correctly).  Replaces zero(x) / fill!(x, 0) of a device
+   buffer (the reference's zeroed gradients, ext/FemtoChatEnzymeExt.jl). */
+fc_status fc_fill_zero(void* dst, size_t bytes, void* stream);
+
 /* Last error message of the calling thread ("" if none). */
 const char* fc_last_error(void);
 

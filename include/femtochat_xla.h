@@ -39,7 +39,10 @@ fc_xla_callback fc_xla_bind_attention_fwd(const fc_attn_desc* desc, int32_t has_
    (ext/FemtoChatReactantExt.jl:176-185; the gradients are overwritten):
    buffers = (dO, Q, K, V, O, l, m, [positions,] dQ, dK, dV[, workspace]).
    *workspace_bytes receives the size of the trailing workspace buffer the
-   call site must declare as an extra output (0: no workspace buffer). */
+   call site must declare as an extra output (0: no workspace buffer).  The
+   buffer needs no more alignment than XLA gives (64 bytes): the size includes
+   255 bytes of slack and the callback works from the buffer's first 256-byte
+   boundary, which fc_attn_bwd requires. */
 fc_xla_callback fc_xla_bind_attention_bwd(const fc_attn_desc* desc, int32_t has_positions,
                                           size_t* workspace_bytes);
 

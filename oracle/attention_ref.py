@@ -80,8 +80,23 @@ def forward(Q, K, V, window, positions=None):
     return O, l, m
 
 
-def backward(dO, Q, K, V, O, l, m, window, positions=None):
-    """Returns (dQ, dK, dV) in float64 (the increments Δflash_attention₁! adds)."""
+def round_bf16(x) -> np.ndarray:
+    """x rounded to bfloat16 (through float32, then to nearest even), as
+    float64 values: the rounding the fast kernels apply to fp32 values."""
+    f = np.asarray(x, dtype=np.float64).astype(np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def backward(dO, Q, K, V, O, l, m, window, positions=None, fast=False):
+    """Returns (dQ, dK, dV) in float64 (the increments Δflash_attention₁! adds).
+
+    fast=True restates the rounding of the reference's tensor-core backward
+    (ext/FemtoChatCUDAExt.jl:1915-1946): P is rounded to bf16 before
+    dV += P^T dO, dS = P (dP - D) is formed from the unrounded P and rounded to
+    bf16 before both dK and dQ, and a query with a single visible key has
+    dS = 0 (:1929-1930)."""
     dO, Q, K, V, O, l, m = map(_f64, (dO, Q, K, V, O, l, m))
     B, T, H, D = Q.shape
     Hkv = K.shape[2]
@@ -99,10 +114,12 @@ def backward(dO, Q, K, V, O, l, m, window, positions=None):
                 P = np.where(vis, np.exp(np.where(vis, S, 0.0) - m[b, h][:, None]), 0.0)
             P = P / np.maximum(l[b, h], EPS_F32)[:, None]
             dOh = dO[b, :, h, :]
-            dV[b, :, kv, :] += P.T @ dOh
+            dV[b, :, kv, :] += (round_bf16(P) if fast else P).T @ dOh
             dP = dOh @ V[b, :, kv, :].T
             Dq = (dOh * O[b, :, h, :]).sum(axis=1)
             dS = P * (dP - Dq[:, None])
+            if fast:
+                dS = round_bf16(np.where((vis.sum(axis=1) > 1)[:, None], dS, 0.0))
             dQ[b, :, h, :] += tau * (dS @ K[b, :, kv, :])
             dK[b, :, kv, :] += tau * (dS.T @ Q[b, :, h, :])
     return dQ, dK, dV

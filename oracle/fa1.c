@@ -2,12 +2,13 @@
  * Float32 restatement of femtochat's blocked FlashAttention-1 CPU path.
  *
  * TEST INFRASTRUCTURE ONLY: used by tests/ to cross-check the float64 oracle
- * (oracle/attention_ref.py) and by bench.py's cpu_baseline leg as the
- * reference CPU algorithm timed on the host.  Nothing in femtochat_amd calls it.
+ * (oracle/attention_ref.py).  Its products are scalar loops; the CPU baseline
+ * bench.py times is oracle/fa1_blas.py, the same algorithm with BLAS
+ * products as the reference's mul! calls.  Nothing in femtochat_amd calls it.
  *
  * fa1_forward restates flash_attention₁! (src/kernels.jl:131-219):
  *   512-wide key blocks (outer) x 512-wide query blocks (inner), no block
- *   skipping; S = K_j^T Q_i * (1/sqrt(D)); masked entries = -floatmax
+ *   skipping and no skipping of masked (zero) entries inside a block; S = K_j^T Q_i * (1/sqrt(D)); masked entries = -floatmax
  *   (:150, :194); block max m~ over the whole column (masked included),
  *   P~ = mask ? exp(S - m~) : 0, l~ = sum P~; m_new = max(m, m~);
  *   l_new = e^(m-m_new) l + e^(m~-m_new) l~; O re-normalised every block:
@@ -114,7 +115,6 @@ static void forward_head(const dims* z, int b, int h, const float* Q, const floa
         for (int d = 0; d < D; ++d) ot[d] = 0.0f;
         for (int kk = 0; kk < nj; ++kk) {
           const float p = row[kk];
-          if (p == 0.0f) continue;
           const float* v = Vb + (long)(j0 + kk) * kp;
           for (int d = 0; d < D; ++d) ot[d] += p * v[d];
         }
@@ -201,7 +201,6 @@ static void backward_group(const dims* z, int b, int kv, const float* dO, const 
           float* dqv = dQb + (long)q * qp;
           for (int kk = 0; kk < nj; ++kk) {
             const float p = prow[kk], ds = srow[kk];
-            if (p == 0.0f && ds == 0.0f) continue;
             float* dvv = dVb + (long)(j0 + kk) * kp;
             float* dkv = dKb + (long)(j0 + kk) * kp;
             const float* kvv = Kb + (long)(j0 + kk) * kp;

@@ -191,3 +191,44 @@ def test_embedding_rejects_bad_descriptors():
         assert lib.fc_embedding_bwd(ctypes.byref(e), fake, fake, fake, None) == L.FC_ERR_INVALID_ARGUMENT, field
     assert lib.fc_embedding_fwd(ctypes.byref(d), None, fake, fake, None) == L.FC_ERR_INVALID_ARGUMENT
     assert lib.fc_embedding_bwd(ctypes.byref(d), fake, None, fake, None) == L.FC_ERR_INVALID_ARGUMENT
+
+
+def test_fast_mode_rejects_slices_past_32_bit_offsets():
+    # The fast kernels address one (batch, head) slice with 32-bit buffer
+    # offsets: (T-1)*H*D*2 + 2*D bytes must stay below 2^31.
+    lib = L.lib()
+    D, H = 128, 10
+    t_max = ((1 << 31) - 2 * D - 1) // (H * D * 2) + 1  # largest T whose slice fits
+    st, _ = ws_bytes(desc(D=D, H=H, Hkv=5, T=t_max, B=1))
+    assert st == L.FC_OK, lib.fc_last_error().decode()
+    st, _ = ws_bytes(desc(D=D, H=H, Hkv=5, T=t_max + 1, B=1))
+    assert st == L.FC_ERR_UNSUPPORTED and "2^31" in lib.fc_last_error().decode()
+    fake = ctypes.c_void_p(0x1000)
+    d = desc(D=D, H=H, Hkv=5, T=t_max + 1, B=1)
+    assert lib.fc_attn_fwd(ctypes.byref(d), fake, fake, fake, None, fake, fake, fake, None, 0, None) == \
+        L.FC_ERR_UNSUPPORTED
+    # exact mode addresses with 64-bit offsets and has no such bound
+    st, _ = ws_bytes(desc(D=D, H=H, Hkv=5, T=t_max + 1, B=1, mode=L.FC_MODE_EXACT, in_dtype=L.FC_F32,
+                          out_dtype=L.FC_F32, dout_dtype=L.FC_F32, grad_dtype=L.FC_F32))
+    assert st == L.FC_OK
+
+
+def test_grouped_polar_express_checks_every_stack_before_launching():
+    # The second stack's workspace is too small: the call fails on the host
+    # with FC_ERR_WORKSPACE before the first stack is enqueued (no GPU needed).
+    lib = L.lib()
+    descs = (L.PolarDesc * 2)()
+    for d in descs:
+        d.m, d.n, d.count, d.steps, d.dtype = 64, 32, 2, 5, L.FC_F32
+    need = ctypes.c_size_t(0)
+    assert lib.fc_polar_workspace_bytes(ctypes.byref(descs[0]), ctypes.byref(need)) == L.FC_OK
+    fake = ctypes.c_void_p(0x100000)
+    G = (ctypes.c_void_p * 2)(fake, fake)
+    ws = (ctypes.c_void_p * 2)(fake, fake)
+    nbytes = (ctypes.c_size_t * 2)(need.value, need.value - 1)
+    st = lib.fc_polar_express_grouped(2, descs, G, ws, nbytes, None)
+    assert st == L.FC_ERR_WORKSPACE and str(need.value) in lib.fc_last_error().decode()
+    nbytes = (ctypes.c_size_t * 2)(need.value, need.value)
+    ws = (ctypes.c_void_p * 2)(fake, ctypes.c_void_p(0x100040))
+    st = lib.fc_polar_express_grouped(2, descs, G, ws, nbytes, None)
+    assert st == L.FC_ERR_WORKSPACE and "aligned" in lib.fc_last_error().decode()

@@ -136,6 +136,25 @@ def test_fused_matches_oracle(gpu, V, reduction, accumulate):
     assert np.array_equal(d[~keep], base.numpy()[~keep])  # ignored columns untouched
 
 
+def test_fused_keeps_a_caller_count(gpu):
+    # A count normalised over several micro-batches (here 3x the local one)
+    # scales the gradient and is left as the caller passed it; the reduced
+    # mean is the local one, as cross_entropy_ reports it.
+    N, V = 29, 4096
+    x, t, xd, td = _ce_case(gpu, N, V, seed=77)
+    local = float((t != -1).sum())
+    count = torch.tensor([3.0 * local], device=gpu)
+    losses, reduced = torch.empty(N, device=gpu), torch.empty(1, device=gpu)
+    delta = torch.zeros(N, V, device=gpu)
+    cross_entropy_fused_(losses, delta, xd, td, 1.0, -1, "mean", reduced=reduced, count=count)
+    torch.cuda.synchronize()
+    assert float(count) == 3.0 * local
+    assert abs(float(reduced) - O.cross_entropy(x.numpy(), t.numpy(), -1, "mean", 0)) < TOL
+    gref = O.cross_entropy_gradient(np.zeros((N, V)), x.numpy(), t.numpy(), 1.0, -1, "mean", 0) / 3.0
+    keep = (t != -1).numpy()
+    assert rel_err(delta.cpu().numpy()[keep], gref[keep]) < TOL
+
+
 def test_fused_rejects_what_it_cannot_hold(gpu):
     x, t, xd, td = _ce_case(gpu, 4, 53, seed=1)
     with pytest.raises(_lib.AttentionError, match="multiple of 4"):

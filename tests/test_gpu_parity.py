@@ -2,10 +2,17 @@
 
 Small cases cover every code path (head dims, GQA ratios, ragged T, windows
 including empty rows, document masks, both modes, bf16/fp32 storage); the
-full-size BASELINE workloads C1..C5 are checked on a subset of (batch, KV
-group) slices against the oracle and through size-independent properties.
+committed golden fixtures are reproduced; the full-size BASELINE workloads
+C1..C5 are checked against the oracle on (batch, KV group) slices in every
+residue class of the kernels' grid rows mod 8 (the XCD a row runs on) plus a
+middle batch row, and over the whole output through size-independent
+properties: the sum identities of dV and dK, the scale identity
+<dQ, Q> = <dK, K> per (batch, KV group), and the closed form of every row
+whose query sees a single key (the first query of a row, every document
+start): O = V, l = 1, m = tau q.k, dQ = 0.
 """
 import zlib
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -256,6 +263,47 @@ def _oracle_slice(h, b, kv, G, window, O_gpu, l_gpu, m_gpu):
 # (measured: 1e-7 to 4e-7 exact, 2e-4 to 6e-4 fast, on C1..C5; a dropped tile
 # moves them by about its share of the keys, 1e-2 and more)
 IDENTITY_TOL = {"exact": 1e-5, "fast": 4e-3}
+# Scale identity |<dQ,Q> - <dK,K>| / (sum|dQ Q| + sum|dK K|) per (batch, KV
+# group): the rounding of dS to bf16 (fast) or fp32 noise (exact); a dropped
+# block of dQ or dK moves it by 1e-4 and more (tests/test_oracle.py).
+SCALE_TOL = {"exact": 1e-5, "fast": 1e-2}
+
+
+def _units(B, Hkv):
+    """(batch, KV group) units whose grid row b*Hkv + kv covers every residue
+    mod 8, plus the first, the last and a middle batch row."""
+    n = B * Hkv
+    picks = {0, n - 1, (B // 2) * Hkv + Hkv // 2}
+    if n >= 8:
+        span = n // 8
+        picks |= {r + 8 * ((3 * r + 1) % span) for r in range(8)}
+    else:
+        picks |= set(range(n))
+    return sorted((u // Hkv, u % Hkv) for u in picks if u < n)
+
+
+def _scale_identity(dQ, Q, dK, K, G):
+    B, T, H, D = Q.shape
+    Hkv = K.shape[2]
+    qq = (dQ.double() * Q.double()).reshape(B, T, Hkv, G, D)
+    kk = dK.double() * K.double()
+    num = (qq.sum(dim=(1, 3, 4)) - kk.sum(dim=(1, 3))).abs()
+    den = qq.abs().sum(dim=(1, 3, 4)) + kk.abs().sum(dim=(1, 3))
+    return (num / den.clamp_min(1e-300)).max().item()
+
+
+def _single_key_rows(h, window):
+    """(b, q) of every query that sees exactly one key (itself): the first
+    query of a row and, with positions, every document start."""
+    out = []
+    B, T = h.Q.shape[0], h.Q.shape[1]
+    for b in range(B):
+        qs = [0] if h.positions is None else list(np.nonzero(h.positions[b] == 0)[0]) + [0]
+        for q in sorted(set(int(x) for x in qs)):
+            vis = R.visible(T, window, None if h.positions is None else h.positions[b])[q]
+            if vis.sum() == 1 and vis[q]:
+                out.append((b, q))
+    return out
 
 
 @pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
@@ -287,18 +335,59 @@ def test_baseline_workload(gpu, name):
         eK = (dK.double().sum(dim=1).abs() / dK.double().abs().sum(dim=1).clamp_min(1e-30)).max().item()
         say(f"  sum dV vs sum dO {eV:.2e}, |sum dK| / sum |dK| {eK:.2e}")
         assert eV <= IDENTITY_TOL[wl.mode] and eK <= IDENTITY_TOL[wl.mode]
-        rows = sorted({0, wl.B - 1})
-        groups = sorted({0, wl.Hkv - 1})
-        for b in rows:
-            for kv in groups:
-                heads = list(range(kv * G, (kv + 1) * G))
-                (O_r, l_r, m_r), (dQ_r, dK_r, dV_r) = _oracle_slice(h, b, kv, G, h.window, On, ln, mn)
-                eO = rel_err(On[b:b + 1][:, :, heads], O_r)
-                eL = lse_err(ln[b:b + 1][:, heads], mn[b:b + 1][:, heads], l_r, m_r)
-                e = [rel_err(gn[0][b:b + 1][:, :, heads], dQ_r), rel_err(gn[1][b:b + 1][:, :, kv:kv + 1], dK_r),
-                     rel_err(gn[2][b:b + 1][:, :, kv:kv + 1], dV_r)]
-                say(f"  b={b} kv={kv}: O {eO:.2e} LSE {eL:.2e} dQ {e[0]:.2e} dK {e[1]:.2e} dV {e[2]:.2e}")
-                assert eO <= tol and eL <= TOL_LSE and max(e) <= tol
+        eS = _scale_identity(dQ, Qd, dK, Kd, G)
+        say(f"  scale identity <dQ,Q> - <dK,K> {eS:.2e}")
+        assert eS <= SCALE_TOL[wl.mode]
+        # Rows whose query sees a single key, over every (batch, head).
+        rows1 = _single_key_rows(h, h.window)
+        assert rows1, "every row's first query sees one key"
+        bi = np.array([r[0] for r in rows1])
+        qi = np.array([r[1] for r in rows1])
+        kvh = np.arange(wl.H) // G
+        Vsel = h.V[bi, qi][:, kvh]  # (n, H, D)
+        Osel = On[bi, qi]
+        tau = 1.0 / np.sqrt(wl.D)
+        m_ref = tau * np.einsum("nhd,nhd->nh", h.Q[bi, qi].astype(np.float64), h.K[bi, qi][:, kvh].astype(np.float64))
+        assert np.max(np.abs(Osel - Vsel)) <= 1e-6 * max(1.0, float(np.abs(Vsel).max())), "O = V at single-key rows"
+        assert np.all(np.abs(ln[bi, :, qi] - 1.0) <= 1e-6), "l = 1 at single-key rows"
+        assert np.max(np.abs(mn[bi, :, qi] - m_ref) / np.maximum(1.0, np.abs(m_ref))) <= 1e-5, "m = tau q.k"
+        dq1 = np.abs(gn[0][bi, qi]).max()
+        assert dq1 <= 1e-5 * max(float(np.abs(gn[0]).max()), 1e-30), f"dQ = 0 at single-key rows ({dq1})"
+        say(f"  {len(rows1)} single-key rows x {wl.H} heads: O = V, l = 1, m = tau q.k, dQ = 0")
+        for b, kv in _units(wl.B, wl.Hkv):
+            heads = list(range(kv * G, (kv + 1) * G))
+            (O_r, l_r, m_r), (dQ_r, dK_r, dV_r) = _oracle_slice(h, b, kv, G, h.window, On, ln, mn)
+            eO = rel_err(On[b:b + 1][:, :, heads], O_r)
+            eL = lse_err(ln[b:b + 1][:, heads], mn[b:b + 1][:, heads], l_r, m_r)
+            e = [rel_err(gn[0][b:b + 1][:, :, heads], dQ_r), rel_err(gn[1][b:b + 1][:, :, kv:kv + 1], dK_r),
+                 rel_err(gn[2][b:b + 1][:, :, kv:kv + 1], dV_r)]
+            say(f"  b={b} kv={kv}: O {eO:.2e} LSE {eL:.2e} dQ {e[0]:.2e} dK {e[1]:.2e} dV {e[2]:.2e}")
+            assert eO <= tol and eL <= TOL_LSE and max(e) <= tol
+
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.mark.parametrize("name", ["c1_golden.npz", "slice_golden.npz"])
+def test_golden_fixtures(gpu, name):
+    # The committed fixtures (tests/golden/make_golden.py): C1 in exact mode,
+    # the document-masked C3 slice (bf16 inputs) in fast mode.
+    z = np.load(GOLDEN / name)
+    fast = name.startswith("slice")
+    mode = "fast" if fast else "exact"
+    A = MFMAFast() if fast else MFMAExact()
+    window = tuple(int(w) for w in z["window"])
+    say(f"golden {name} window {window}")
+    Qd, Kd, Vd, dOd = (_dev(z[k], fast, gpu) for k in ("Q", "K", "V", "dO"))
+    pos_d = torch.from_numpy(z["positions"].astype(np.int32)).to(gpu)
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, window, pos_d)
+    dQ, dK, dV = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, window, pos_d)
+    torch.cuda.synchronize()
+    tol = TOL[mode]
+    assert rel_err(to_np(O), z["O"]) <= tol
+    assert lse_err(to_np(l), to_np(m), z["l"], z["m"]) <= TOL_LSE
+    for k, x in (("dQ", dQ), ("dK", dK), ("dV", dV)):
+        assert rel_err(to_np(x), z[k]) <= tol, k
 
 
 @pytest.mark.parametrize("growth", [40.0, 140.0])
@@ -329,15 +418,16 @@ def test_fast_forward_large_logit_growth(gpu, growth):
     L = to_np(m).astype(np.float64) + np.log(to_np(l).astype(np.float64))
     L_ref = m_ref + np.log(l_ref)
     assert np.max(np.abs(L - L_ref) / np.maximum(1.0, np.abs(L_ref))) <= TOL_LSE
-    if growth > 64:
-        # Keys here share a common component near 6 and dS sums to zero
-        # along a row, so fast mode's bf16 rounding of dS (as the
-        # reference's) leaves a few percent in dQ against the unrounded
-        # float64 oracle: the backward is checked on the milder case.
-        return
     dOd = _dev(dO, True, gpu)
     grads = gpu_backward(MFMAFast(), dOd, Qd, Kd, Vd, O, l, m, (-1, 0))
     torch.cuda.synchronize()
-    g_ref = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), (-1, 0))
+    # Keys here share a common component near 6 and dS sums to zero along a
+    # row, so at growth 140 fast mode's bf16 rounding of dS (as the
+    # reference's) leaves a few percent in dQ against the unrounded float64
+    # oracle; the oracle that rounds P and dS as the reference's tensor-core
+    # backward does is the one to match.
+    g_ref = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), (-1, 0), fast=growth > 64)
     for name, x, r in zip(("dQ", "dK", "dV"), grads, g_ref):
-        assert rel_err(to_np(x), r) <= TOL["fast"], name
+        e = rel_err(to_np(x), r)
+        say(f"  {name} rel err {e:.2e}")
+        assert e <= TOL["fast"], name

@@ -17,8 +17,15 @@ def test_window_sizes_reference_semantics():
     assert window_sizes(2048, 3, "S") == [(512, 0), (512, 0), (2048, 0)]
     assert window_sizes(1000, 2, "SL") == [(256, 0), (1000, 0)]
     assert window_sizes(100, 1, "S") == [(100, 0)]
+    # The reference tests `== 'S'` only: every other character is a long layer.
+    assert window_sizes(2048, 4, "SXsL") == [(512, 0), (2048, 0), (2048, 0), (2048, 0)]
+    assert window_sizes(2048, 3, "x") == [(2048, 0)] * 3
+    assert window_sizes(2048, 5, "SL") == [(512, 0), (2048, 0), (512, 0), (2048, 0), (2048, 0)]
+    # mod1(i, 0) and windows[end] on an empty list fail in the reference too.
     with pytest.raises(ValueError):
-        window_sizes(2048, 2, "SX")
+        window_sizes(2048, 2, "")
+    with pytest.raises(ValueError):
+        window_sizes(2048, 0, "S")
 
 
 def test_visible_pairs_matches_mask_count():

@@ -12,7 +12,13 @@ a transposed operand, an off-by-one window, a wrong GQA head map) fails:
 * closed forms and invariants: T=1, single visible key, causal sentinel,
   V scaling, softmax normalisation, GQA == repeated K/V, document mask ==
   per-segment attention, batch/head permutation;
-* the committed golden fixture for C1 (tests/golden/c1_golden.npz).
+* the committed golden fixtures (tests/golden/c1_golden.npz and the
+  document-masked C3 slice, slice_golden.npz);
+* the scale identity <dQ, Q> = <dK, K> per (batch, KV group) that the
+  full-size GPU tests check (Q -> aQ, K -> K/a leaves the output unchanged);
+* the fast-mode rounding variant of the backward (P and dS rounded to bf16):
+  its rounding against torch's bfloat16 conversion, and exact agreement with
+  the unrounded backward on inputs whose P and dS are bf16 values.
 """
 from pathlib import Path
 
@@ -23,8 +29,10 @@ import torch
 from femtochat_amd import workloads as W
 from oracle import attention_ref as R
 from oracle import fa1
+from oracle import fa1_blas
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "c1_golden.npz"
+SLICE_GOLDEN = Path(__file__).resolve().parent / "golden" / "slice_golden.npz"
 
 
 def rand(seed, B, T, H, Hkv, D):
@@ -188,6 +196,82 @@ def test_backward_sum_identities(case):
     assert np.max(np.abs(dK_bad.sum(axis=1)) / np.abs(dK).sum(axis=1)) > 1e-3
 
 
+def scale_identity_error(dQ, Q, dK, K, G):
+    """max over (batch, KV group) of |<dQ, Q> - <dK, K>| / (sum|dQ Q| + sum|dK K|)."""
+    B, T, H, D = Q.shape
+    Hkv = K.shape[2]
+    qq = (dQ * Q).reshape(B, T, Hkv, G, D)
+    kk = dK * K
+    num = np.abs(qq.sum(axis=(1, 3, 4)) - kk.sum(axis=(1, 3)))
+    den = np.abs(qq).sum(axis=(1, 3, 4)) + np.abs(kk).sum(axis=(1, 3))
+    return float(np.max(num / np.maximum(den, 1e-300)))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(c[0]) for c in CASES])
+def test_backward_scale_identity(case):
+    # O(aQ, K/a) = O(Q, K) for every mask, so d/da at a = 1 gives
+    # sum <dQ, Q> = sum <dK, K> per (batch, KV group), over every token: the
+    # identity the full-size GPU tests check on the whole output.  A planted
+    # error (the dQ or the dK of one block of tokens dropped) must break it.
+    seed, B, T, H, Hkv, D, window, pos_kind = case
+    Q, K, V, dO = rand(seed, B, T, H, Hkv, D)
+    pos = _positions(seed, B, T) if pos_kind == "docs" else None
+    O, l, m = R.forward(Q, K, V, window, pos)
+    dQ, dK, dV = R.backward(dO, Q, K, V, O, l, m, window, pos)
+    G = H // Hkv
+    assert scale_identity_error(dQ, Q, dK, K, G) < 1e-12
+    dQ_bad = dQ.copy()
+    dQ_bad[:, T // 2:] = 0.0
+    assert scale_identity_error(dQ_bad, Q, dK, K, G) > 1e-4
+    dK_bad = dK.copy()
+    dK_bad[:, T // 2:] = 0.0
+    assert scale_identity_error(dQ, Q, dK_bad, K, G) > 1e-4
+    # The fast-mode rounding keeps it to the bf16 rounding of dS.
+    gq, gk, _ = R.backward(dO, Q, K, V, O, l, m, window, pos, fast=True)
+    assert scale_identity_error(gq, Q, gk, K, G) < 2e-2
+
+
+def test_round_bf16_matches_torch():
+    rng = np.random.Generator(np.random.PCG64(5))
+    x = np.concatenate([rng.standard_normal(10000) * 10.0 ** rng.integers(-30, 30, 10000),
+                        # exact ties between two bf16 values, both parities
+                        np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 2.0 ** -130, 0.0, -0.0])])
+    x32 = x.astype(np.float32)
+    ref = torch.from_numpy(x32).to(torch.bfloat16).to(torch.float64).numpy()
+    got = R.round_bf16(x32)
+    assert np.array_equal(got.view(np.int64), ref.view(np.int64))
+
+
+def test_fast_backward_rounding():
+    # (a) On inputs whose probabilities and dS are bf16 values the rounding
+    # changes nothing: each query sees two keys of equal score (P = 1/2) and
+    # dO, V hold small integers (dP - D is then exact in bf16).
+    T, D = 8, 16
+    Q = np.zeros((1, T, 1, D))
+    K = np.zeros((1, T, 1, D))
+    rng = np.random.Generator(np.random.PCG64(3))
+    V = rng.integers(-3, 4, (1, T, 1, D)).astype(np.float64)
+    dO = rng.integers(-3, 4, (1, T, 1, D)).astype(np.float64)
+    window = (1, 0)  # keys q-1 and q (query 0 sees one key)
+    O, l, m = R.forward(Q, K, V, window)
+    exact = R.backward(dO, Q, K, V, O, l, m, window)
+    fast = R.backward(dO, Q, K, V, O, l, m, window, fast=True)
+    for a, b in zip(fast, exact):
+        assert np.array_equal(a, b)
+    # (b) In general it moves the gradients by the bf16 rounding of P and dS:
+    # about 2^-9 relative, and not zero.
+    Q, K, V, dO = rand(4, 1, 40, 2, 1, 32)
+    O, l, m = R.forward(Q, K, V, (-1, 0))
+    exact = R.backward(dO, Q, K, V, O, l, m, (-1, 0))
+    fast = R.backward(dO, Q, K, V, O, l, m, (-1, 0), fast=True)
+    for a, b in zip(fast, exact):
+        e = max_rel(a, b)
+        assert 1e-5 < e < 2e-2
+    # (c) dV uses the rounded P and dK the rounded dS: a backward that rounds
+    # only dS (P unrounded in dV) differs from it.
+    assert max_rel(fast[2], exact[2]) > 1e-5
+
+
 def test_document_mask_equals_segments():
     T, H, Hkv, D = 30, 2, 1, 16
     lengths = [7, 1, 12, 10]
@@ -257,6 +341,30 @@ def test_fa1_restatement_matches_oracle(window, T, pos):
         assert max_rel(a, 2 * b) < 1e-5  # fp32 sums in a different order
 
 
+@pytest.mark.parametrize("window,T,pos", [((-1, 0), 700, False), ((100, 0), 600, False), ((50, 20), 530, False),
+                                          ((-1, 0), 650, True)])
+def test_blas_restatement_matches_oracle(window, T, pos):
+    # oracle/fa1_blas.py, the CPU baseline bench.py times: the reference's
+    # blocked algorithm with BLAS products, float32.
+    B, H, Hkv, D = 2, 4, 2, 32
+    Q, K, V, dO = (x.astype(np.float32) for x in rand(91 + T, B, T, H, Hkv, D))
+    positions = W.document_positions(T, B, seed=T, mean=150, sigma=1.0, cap=400) if pos else None
+    O, l, m = R.forward(Q, K, V, window, positions)
+    O1, l1, m1 = fa1_blas.forward(Q, K, V, window, positions)
+    assert max_rel(O1, O) < 1e-5
+    assert np.max(np.abs(R.lse(l1, m1) - R.lse(l, m))) < 1e-5
+    g = R.backward(dO, Q, K, V, O, l, m, window, positions)
+    g1 = fa1_blas.backward(dO, Q, K, V, O1, l1, m1, window, positions)
+    for a, b in zip(g1, g):
+        assert max_rel(a, b) < 1e-5
+    # It accumulates like Δflash_attention₁!.
+    g2 = fa1_blas.backward(dO, Q, K, V, O1, l1, m1, window, positions, *(x.copy() for x in g1))
+    for a, b in zip(g2, g1):
+        assert max_rel(a, 2 * b) < 1e-5
+    # Its statistics are the reference's: m the row max over visible keys.
+    assert max_rel(m1[l > 0], m[l > 0]) < 1e-6
+
+
 def test_golden_fixture_c1():
     """The committed C1 vectors (generated by tests/golden/make_golden.py) are reproduced."""
     z = np.load(GOLDEN)
@@ -269,6 +377,21 @@ def test_golden_fixture_c1():
     g = R.backward(z["dO"], z["Q"], z["K"], z["V"], z["O"], z["l"], z["m"], tuple(z["window"]), z["positions"])
     for name, x in zip(("dQ", "dK", "dV"), g):
         assert np.allclose(x, z[name], rtol=0, atol=1e-12)
+
+
+def test_golden_fixture_slice():
+    """The committed C3-shaped slice (document mask, window (20,0), bf16 inputs) is reproduced."""
+    z = np.load(SLICE_GOLDEN)
+    window = tuple(int(w) for w in z["window"])
+    O, l, m = R.forward(z["Q"], z["K"], z["V"], window, z["positions"])
+    assert np.allclose(O, z["O"], rtol=0, atol=1e-6)  # stored as float32
+    assert np.allclose(l, z["l"], rtol=0, atol=1e-12) and np.allclose(m, z["m"], rtol=0, atol=1e-12)
+    g = R.backward(z["dO"], z["Q"], z["K"], z["V"], O, l, m, window, z["positions"])
+    for name, x in zip(("dQ", "dK", "dV"), g):
+        assert np.allclose(x, z[name], rtol=0, atol=1e-6 * max(1.0, float(np.abs(x).max())))
+    # bf16 inputs: every value is a bfloat16 number
+    for name in ("Q", "K", "V", "dO"):
+        assert np.array_equal(R.round_bf16(z[name]), z[name].astype(np.float64))
 
 
 PLANTED = {

@@ -171,6 +171,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(AttnDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
     ),
+    "fc_attn_bwd_noalloc": (
+        ctypes.c_int,
+        [ctypes.POINTER(AttnDesc), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    ),
     "fc_rope_norm_fwd": (ctypes.c_int, [ctypes.POINTER(RopeNormDesc), _P, _P, _P, _P, _P, _P]),
     "fc_rope_norm_bwd": (ctypes.c_int, [ctypes.POINTER(RopeNormDesc), _P, _P, _P, _P, _P, _P, _P]),
     "fc_cross_entropy_fwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _P, _P, _P, _P, _P, _P, _P]),

@@ -166,24 +166,31 @@ fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, co
   return ok();
 }
 
-fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, const void* K, const void* V,
-                      const void* O, const float* l, const float* m, const int32_t* positions, void* dQ,
-                      void* dK, void* dV, void* workspace, size_t workspace_bytes, void* stream) {
-  fc::Problem p;
-  fc_status st = make_problem(desc, &p);
+}  // extern "C"
+
+namespace {
+
+// Validation the two backward entry points share: the problem, the pointers.
+fc_status bwd_problem(const char* who, const fc_attn_desc* desc, const void* dO, const void* Q, const void* K,
+                      const void* V, const void* O, const float* l, const float* m, const int32_t* positions,
+                      const void* dQ, const void* dK, const void* dV, fc::Problem* p) {
+  const fc_status st = make_problem(desc, p);
   if (st != FC_OK) return st;
   if (dO == nullptr || Q == nullptr || K == nullptr || V == nullptr || O == nullptr || l == nullptr ||
       m == nullptr || dQ == nullptr || dK == nullptr || dV == nullptr)
-    return fail(FC_ERR_INVALID_ARGUMENT, "fc_attn_bwd: a required pointer is null");
-  p.positions = positions != nullptr;
+    return fail(FC_ERR_INVALID_ARGUMENT, "%s: a required pointer is null", who);
+  p->positions = positions != nullptr;
+  return FC_OK;
+}
+
+// Launches the backward of a validated problem with its workspace at w
+// (bwd_workspace(p).total bytes, 256-byte aligned).  Every workspace byte the
+// kernels read is written earlier in the same sequence, so the workspace
+// needs no clearing.
+fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const void* K, const void* V,
+                     const void* O, const float* l, const float* m, const int32_t* positions, void* dQ, void* dK,
+                     void* dV, char* w, hipStream_t s) {
   const fc::BwdWorkspace ws = fc::bwd_workspace(p);
-  if (workspace == nullptr || workspace_bytes < ws.total)
-    return fail(FC_ERR_WORKSPACE, "backward workspace needs %zu bytes, got %zu%s", ws.total, workspace_bytes,
-                workspace == nullptr ? " (null)" : "");
-  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
-    return fail(FC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  char* w = static_cast<char*>(workspace);
 
   // Fast mode with bf16 O and dO: the dQ kernel computes the preprocess
   // itself and runs first; otherwise a preprocess launch (which also makes
@@ -257,6 +264,85 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, c
   e = fc::launch_bwd_dq(p, a, s);
   if (e != hipSuccess) return fail(FC_ERR_HIP, "dQ launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, const void* K, const void* V,
+                      const void* O, const float* l, const float* m, const int32_t* positions, void* dQ,
+                      void* dK, void* dV, void* workspace, size_t workspace_bytes, void* stream) {
+  fc::Problem p;
+  const fc_status st = bwd_problem("fc_attn_bwd", desc, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, &p);
+  if (st != FC_OK) return st;
+  const fc::BwdWorkspace ws = fc::bwd_workspace(p);
+  if (workspace == nullptr || workspace_bytes < ws.total)
+    return fail(FC_ERR_WORKSPACE, "backward workspace needs %zu bytes, got %zu%s", ws.total, workspace_bytes,
+                workspace == nullptr ? " (null)" : "");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(FC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return bwd_launch(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, static_cast<char*>(workspace),
+                    static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+// Backward scratch of fc_attn_bwd_noalloc.  Each GPU the library runs on
+// holds its own copy from the code object's load until the process ends.  In
+// host code `scratch` names a host-side stand-in, never the device memory:
+// the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char scratch[FC_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxScratchDevices] = {};  // device ordinal -> that device's scratch
+
+// The current device's scratch address, looked up on the first call on that
+// device (with the device current, as hipGetSymbolAddress requires).
+fc_status current_scratch(char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FC_ERR_HIP, "fc_attn_bwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(FC_ERR_UNSUPPORTED, "fc_attn_bwd_noalloc: device ordinal %d is %d or more", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(FC_ERR_HIP, "fc_attn_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    if ((reinterpret_cast<uintptr_t>(ptr) & 255) != 0)
+      return fail(FC_ERR_HIP, "fc_attn_bwd_noalloc: scratch on device %d is not 256-byte aligned", dev);
+    g_scratch_ptr[dev] = static_cast<char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return FC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+fc_status fc_attn_bwd_noalloc(const fc_attn_desc* desc, const void* dO, const void* Q, const void* K, const void* V,
+                              const void* O, const float* l, const float* m, const int32_t* positions, void* dQ,
+                              void* dK, void* dV, void* stream) {
+  fc::Problem p;
+  fc_status st = bwd_problem("fc_attn_bwd_noalloc", desc, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, &p);
+  if (st != FC_OK) return st;
+  const size_t need = fc::bwd_workspace(p).total;
+  if (need > (size_t)FC_ATTN_NOALLOC_SCRATCH_BYTES)
+    return fail(FC_ERR_WORKSPACE,
+                "fc_attn_bwd_noalloc: the problem needs %zu bytes of scratch, more than the %zu the library holds "
+                "per GPU (call fc_attn_bwd with a workspace instead)",
+                need, (size_t)FC_ATTN_NOALLOC_SCRATCH_BYTES);
+  char* w = nullptr;
+  st = current_scratch(&w);
+  if (st != FC_OK) return st;
+  return bwd_launch(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, w, static_cast<hipStream_t>(stream));
 }
 
 // ---- attention prologue (rope_norm.hip) -----------------------------------

@@ -104,6 +104,24 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q,
                       void* dQ, void* dK, void* dV, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Backward without a workspace argument and without any allocation: the same
+   kernels and results as fc_attn_bwd, with the workspace taken from a scratch
+   array of FC_ATTN_NOALLOC_SCRATCH_BYTES that the library holds on each GPU
+   it runs on until the process ends.  No counterpart in the reference: it is
+   for callers that cannot allocate device memory (code under HIP graph
+   capture, serving loops, harnesses that forbid hipMalloc).  A problem whose
+   fc_attn_workspace_bytes(FC_PASS_BACKWARD) exceeds the limit gets
+   FC_ERR_WORKSPACE.  Every call on one GPU shares that GPU's array: calls
+   that overlap on one GPU (different streams, or threads without ordering)
+   race; calls on one stream are ordered and safe.  The current device must
+   be the stream's device. */
+#define FC_ATTN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+fc_status fc_attn_bwd_noalloc(const fc_attn_desc* desc, const void* dO,
+                              const void* Q, const void* K, const void* V,
+                              const void* O, const float* l, const float* m,
+                              const int32_t* positions, void* dQ, void* dK,
+                              void* dV, void* stream);
+
 /* ---- Attention prologue ---------------------------------------------------
  * Rotary embedding followed by the RMS norm over the head dimension scaled by
  * 1.2, applied to Q or K as CausalSelfAttention does before calling

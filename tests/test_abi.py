@@ -131,6 +131,24 @@ def test_workspace_checks():
     assert st == L.FC_ERR_WORKSPACE and "aligned" in lib.fc_last_error().decode()
 
 
+def test_noalloc_backward_rejects_problems_beyond_its_scratch():
+    # Checked on the host before any HIP call: B*H*T = 2^23 query rows need
+    # 2 * 4 * 2^23 bytes = 64 MiB of statistics, above the 32 MiB scratch.
+    lib = L.lib()
+    fake = ctypes.c_void_p(0x1000)
+    big = desc(D=16, H=128, Hkv=128, T=65536, B=1)
+    st, need = ws_bytes(big)
+    assert st == L.FC_OK and need > 32 << 20
+    st = lib.fc_attn_bwd_noalloc(ctypes.byref(big), fake, fake, fake, fake, fake, fake, fake, None, fake, fake,
+                                 fake, None)
+    assert st == L.FC_ERR_WORKSPACE
+    msg = lib.fc_last_error().decode()
+    assert str(need) in msg and str(32 << 20) in msg
+    st = lib.fc_attn_bwd_noalloc(ctypes.byref(desc()), fake, fake, fake, fake, fake, fake, fake, None, None, fake,
+                                 fake, None)
+    assert st == L.FC_ERR_INVALID_ARGUMENT and "fc_attn_bwd_noalloc" in lib.fc_last_error().decode()
+
+
 def test_last_error_is_cleared_on_success():
     lib = L.lib()
     ws_bytes(desc(H=5, Hkv=2))

@@ -113,10 +113,12 @@ struct DkdvStep {
   // there without a test.
   template <bool need_mask>
   __device__ static inline void softmax(f32x16& s, f32x16& dp, const f32x4* L, const f32x4* Dl, const i32x4* LB,
-                                        const f32x4* Z, int qb, int q0, int key, int g, int right, float c2,
+                                        const f32x4* Z, int qb, int q0, int key, int g, int T, int right, float c2,
                                         bf16x8* pf, bf16x8* sf) {
-    // key - q <= right  <=>  x >= -(8j + t) for row 4g + 8j + t.
-    const int x = q0 + 32 * qb + 4 * g - key + right;
+    // key - q <= right  <=>  x >= -(8j + t) for row 4g + 8j + t; a key at or
+    // past T (the last key tile's padding) fails it for every row, so that
+    // P and dS stay zero there even for a row whose lse2 is -inf.
+    const int x = key < T ? q0 + 32 * qb + 4 * g - key + right : -(1 << 30);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -195,7 +197,7 @@ struct DkdvStep {
         }
       }
       if (bs >= 0 && bs < NQB) {
-        softmax<need_mask>(s[bs], dp[bs], L[bs], Dl[bs], LB[bs], Z[bs], bs, q0, key, g, right, c2, pf[bs],
+        softmax<need_mask>(s[bs], dp[bs], L[bs], Dl[bs], LB[bs], Z[bs], bs, q0, key, g, T, right, c2, pf[bs],
                            sf[bs]);
         // First transposed fragments of the block, for the next phase.
 #pragma unroll

@@ -112,9 +112,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_kt = (T + C::kBK - 1) / C::kBK;
-  const int id = xcd_remap(blockIdx.x, n_kt * a.Hkv * a.B);
-  const int bkv = id / n_kt;
-  const int kt = id - bkv * n_kt;
+  // Key tiles that the most query tiles can see come first, over the whole grid.
+  const GridItem it0 = heavy_first(blockIdx.x, a.Hkv * a.B);
+  const int bkv = it0.row;
+  const int kt = it0.rank;
   const int b = bkv / a.Hkv, kvh = bkv - b * a.Hkv;
   const int k0 = kt * C::kBK;
   const int k1 = min(k0 + C::kBK, T) - 1;
@@ -356,10 +357,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dq_kernel(BwdArgs a) {
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_qt = (T + C::kBM - 1) / C::kBM;
-  const int id = xcd_remap(blockIdx.x, n_qt * a.H * a.B);
-  const int bh = id / n_qt;
-  const int qt = n_qt - 1 - (id - bh * n_qt);
-  const int b = bh / a.H, h = bh - b * a.H;
+  const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
+  const int qt = n_qt - 1 - it0.rank;  // longest query tiles first, over the whole grid
+  int b, h;
+  query_row(it0.row, a.B, a.Hkv, a.group, b, h);
   const int kvh = h / a.group;
 
   const int64_t qpitch = (int64_t)a.H * D, kpitch = (int64_t)a.Hkv * D;

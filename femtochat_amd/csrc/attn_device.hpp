@@ -143,15 +143,6 @@ __device__ inline int wave_max64(int v) {
   return v;
 }
 
-// Spread consecutive workgroup ids over the 8 XCDs so that a run of
-// consecutive logical tiles (which share K/V) lands on one XCD's L2.
-// Hardware dispatches id to XCD id % 8; this returns the logical tile index.
-__device__ inline int xcd_remap(int id, int total) {
-  const int per = total >> 3, rem = total & 7;
-  const int xcd = id & 7, local = id >> 3;
-  return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
-}
-
 // Grid order for (row, tile) work items: all rows' heaviest tiles first
 // (rank 0), then the next heaviest, and so on, so the last workgroups
 // dispatched are the lightest and no long one starts near the end.  Rows

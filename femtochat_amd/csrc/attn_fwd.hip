@@ -52,10 +52,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_qt = (T + C::kBM - 1) / C::kBM;
-  const int id = xcd_remap(blockIdx.x, n_qt * a.H * a.B);
-  const int bh = id / n_qt;
-  const int qt = n_qt - 1 - (id - bh * n_qt);  // longest query tiles first
-  const int b = bh / a.H, h = bh - b * a.H;
+  const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
+  const int qt = n_qt - 1 - it0.rank;  // longest query tiles first, over the whole grid
+  int b, h;
+  query_row(it0.row, a.B, a.Hkv, a.group, b, h);
   const int kvh = h / a.group;
 
   const int64_t qpitch = (int64_t)a.H * D, kpitch = (int64_t)a.Hkv * D;

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -44,6 +45,24 @@ fc_status ok() {
 }  // namespace
 
 namespace fc {
+hipError_t device_cus(int* cus) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < 64 && cache[dev].load(std::memory_order_relaxed) > 0) {
+    *cus = cache[dev].load(std::memory_order_relaxed);
+    return hipSuccess;
+  }
+  int n = 0;
+  e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  if (n <= 0) return hipErrorInvalidDevice;
+  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  *cus = n;
+  return hipSuccess;
+}
+
 // Shared with the other translation units of the library (fc_last_error).
 fc_status set_error(fc_status code, const char* message) {
   g_last_error = message;
@@ -204,6 +223,8 @@ fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const 
   pa.delta = reinterpret_cast<float*>(w + ws.delta);
   pa.lse2 = reinterpret_cast<float*>(w + ws.lse2);
   pa.dO16 = (p.bf16 && !p.dout_bf16) ? w + ws.dO16 : nullptr;
+  int* queue = p.bf16 ? reinterpret_cast<int*>(w + ws.queue) : nullptr;
+  pa.queue = fused_stats ? nullptr : queue;
   pa.H = p.H;
   pa.T = p.T;
   pa.B = p.B;
@@ -232,6 +253,7 @@ fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const 
   a.lse2 = pa.lse2;
   a.pos = positions;
   a.chunk_lb = chunk_lb;
+  a.queue = queue;
   a.dQ = dQ;
   a.dK = dK;
   a.dV = dV;

@@ -240,54 +240,52 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   constexpr int kVisTiles = 256;  // query tiles whose visibility is tabulated in LDS
   __shared__ unsigned char s_vis[kVisTiles];
 
+  __shared__ int s_next;
+
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
-  // Key tiles that the most query tiles can see come first.
-  const GridItem it0 = heavy_first(blockIdx.x, a.Hkv * a.B);
-  const int kt = it0.rank;
-  const int b = it0.row / a.Hkv, kvh = it0.row - b * a.Hkv;
-  const int k0 = kt * C::kBK;
-  const int k1 = min(k0 + C::kBK, T) - 1;
-  const int kw0 = k0 + 32 * wave, kw1 = kw0 + 31;
-  const int key = kw0 + l32;
-
   const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;
   const int64_t qrec = (int64_t)(T - 1) * qpitch + 2 * D;
   const int64_t krec = (int64_t)(T - 1) * kpitch + 2 * D;
-  const char* Kb = static_cast<const char*>(a.K) + (((int64_t)b * T * a.Hkv + kvh) * D) * 2;
-  const char* Vb = static_cast<const char*>(a.V) + (((int64_t)b * T * a.Hkv + kvh) * D) * 2;
-  const int32_t* pos = a.pos ? a.pos + (int64_t)b * T : nullptr;
   const int nchunks = (T + 31) / 32;
-  const int32_t* clb = a.chunk_lb ? a.chunk_lb + (int64_t)b * nchunks * 2 : nullptr;
 
-  // K and V of the wave's 32 keys as B operands (lane = key).
+  // Work items are (key tile, batch, KV head), key tiles that the most query
+  // tiles can see first (item = rank * rows + row).  The grid is one
+  // workgroup per CU; each takes item blockIdx.x first and then the next
+  // unclaimed one, gridDim.x + a counter the preceding kernel zeroed, so the
+  // heaviest items go first and every workgroup stays busy to the end.
+  const int rows = a.Hkv * a.B;
+  const int n_items = ((T + C::kBK - 1) / C::kBK) * rows;
+
+  // K and V of the wave's 32 keys of an item as B operands (lane = key).
+  // The next item's are loaded while this item's dK and dV are stored.
   bf16x8 kf[KC], vf[KC];
-  {
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kb, (uint32_t)krec);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vb, (uint32_t)krec);
-    const int koff = key * kpitch + 16 * g;
+  auto load_kv = [&](int item) {
+    const int row = item % rows, ikt = item / rows;
+    const int ib = row / a.Hkv, ikvh = row - ib * a.Hkv;
+    const int64_t base = (((int64_t)ib * T * a.Hkv + ikvh) * D) * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(static_cast<const char*>(a.K) + base, (uint32_t)krec);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(static_cast<const char*>(a.V) + base, (uint32_t)krec);
+    const int koff = (ikt * C::kBK + 32 * wave + l32) * kpitch + 16 * g;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       kf[c] = as_bf16x8(buf_load16(rk, koff + 32 * c, 0));
       vf[c] = as_bf16x8(buf_load16(rv, koff + 32 * c, 0));
     }
-  }
-  f32x16 dk[DB], dv[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i) {
-    dk[i] = zero16();
-    dv[i] = zero16();
-  }
+  };
 
-  // Query tiles that can see [k0, k1]: q in [k0 - right, k1 + left].
-  const int qlo = max(0, k0 - a.right);
-  const int qhi = min(T - 1, k1 + a.left);
-  const int qt_begin = qlo / BQ;
-  const int n_qt_tiles = qhi >= qlo ? qhi / BQ - qt_begin + 1 : 0;
+  // State of the current item, set by setup(); the step lambdas read it.
+  int b = 0, kvh = 0, k0 = 0, k1 = 0, kw0 = 0, kw1 = 0, key = 0;
+  const int32_t* pos = nullptr;
+  const int32_t* clb = nullptr;
+  int qt_begin = 0, n_qt_tiles = 0, t_first = 0, G = 0;
+  bool vis_table = false;
+  f32x16 dk[DB], dv[DB];  // the item's dK (unscaled) and dV
+
   // With positions, a query tile is skipped when no query of it can see a key
   // of [k0, k1] (its smallest key lower bound exceeds k1).  The answers are
-  // tabulated in LDS up front so the step loop reads no global memory.
+  // tabulated in LDS per item so the step loop reads no global memory.
   auto tile_visible_global = [&](int qt) -> bool {
     const int c0 = (qt * BQ) / 32;
     int lo = clb[2 * c0];
@@ -296,11 +294,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       if (c0 + c < nchunks) lo = min(lo, clb[2 * (c0 + c)]);
     return lo <= k1;
   };
-  const bool vis_table = clb != nullptr && n_qt_tiles <= kVisTiles;
-  if (vis_table) {
-    for (int t = tid; t < n_qt_tiles; t += kThreads) s_vis[t] = tile_visible_global(qt_begin + t) ? 1 : 0;
-  }
-  __syncthreads();
   auto tile_visible = [&](int qt) -> bool {
     if (clb == nullptr) return true;
     return vis_table ? s_vis[qt - qt_begin] != 0 : tile_visible_global(qt);
@@ -314,12 +307,35 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
     while (t < n_qt_tiles && !tile_visible(qt_begin + t)) ++t;
     return t;
   };
-  const int t_first = first_tile(0);
   auto advance = [&](Step s) -> Step {
     const int t = first_tile(s.t + 1);
     return t < n_qt_tiles ? Step{s.h, t} : Step{s.h + 1, t_first};
   };
-
+  // Decodes an item and tabulates its tile visibility (ends with a barrier).
+  auto setup = [&](int it) {
+    const int kt = it / rows;
+    b = (it % rows) / a.Hkv;
+    kvh = (it % rows) - b * a.Hkv;
+    k0 = kt * C::kBK;
+    k1 = min(k0 + C::kBK, T) - 1;
+    kw0 = k0 + 32 * wave;
+    kw1 = kw0 + 31;
+    key = kw0 + l32;
+    pos = a.pos ? a.pos + (int64_t)b * T : nullptr;
+    clb = a.chunk_lb ? a.chunk_lb + (int64_t)b * nchunks * 2 : nullptr;
+    // Query tiles that can see [k0, k1]: q in [k0 - right, k1 + left].
+    const int qlo = max(0, k0 - a.right);
+    const int qhi = min(T - 1, k1 + a.left);
+    qt_begin = qlo / BQ;
+    n_qt_tiles = qhi >= qlo ? qhi / BQ - qt_begin + 1 : 0;
+    vis_table = clb != nullptr && n_qt_tiles <= kVisTiles;
+    if (vis_table) {
+      for (int t = tid; t < n_qt_tiles; t += kThreads) s_vis[t] = tile_visible_global(qt_begin + t) ? 1 : 0;
+    }
+    __syncthreads();
+    t_first = first_tile(0);
+    G = t_first < n_qt_tiles ? a.group : 0;  // no visible tile: no step
+  };
   FragOffsets<D> fo;
   fo.init(lane);
   DmaPlan<D, BQ> plan;
@@ -409,14 +425,34 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
                      fo, q0, key, kw0, kw1, g, T, a.right, c2);
   };
 
-  const int G = t_first < n_qt_tiles ? a.group : 0;  // no visible tile: no step
-  Step st{0, t_first};
-  if (st.h < G) {
-    issue(st, bufA);
+  // The first step of the item set up last: its tile into bufA and its row
+  // statistics into registers (published before the item's first step).
+  auto start = [&]() {
+    if (G > 0) {
+      issue(Step{0, t_first}, bufA);
 #pragma unroll
-    for (int k = 0; k < NPH; ++k) dma_part(k);
-    publish(0);
+      for (int k = 0; k < NPH; ++k) dma_part(k);
+    }
+  };
+
+  int item = blockIdx.x;
+  if (item < n_items) {
+    load_kv(item);
+    setup(item);
+    start();
+    if (G > 0) publish(0);
   }
+  while (item < n_items) {
+  // Claim the next item now; its index is read once this item's steps are done.
+  int claimed = 0;
+  if (tid == 0) claimed = (int)gridDim.x + atomicAdd(a.queue, 1);
+
+#pragma unroll
+  for (int i = 0; i < DB; ++i) {
+    dk[i] = zero16();
+    dv[i] = zero16();
+  }
+  Step st{0, t_first};
   dma_wait_barrier();
   while (st.h < G) {
     const Step st1 = advance(st);
@@ -435,13 +471,25 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
     st = st2;
   }
 
+  if (tid == 0) s_next = claimed;
+  __syncthreads();
+  const int next = s_next;
+  // This item's stores need its row and keys; the next item's K, V, first
+  // tile and row statistics load meanwhile.
+  const int eb = b, ekvh = kvh, ekw0 = kw0;
+  if (next < n_items) {
+    load_kv(next);
+    setup(next);
+    start();
+  }
+
   // Accumulator row = key, column = head-dim index.  The stores go through a
   // buffer descriptor over this (batch, KV head)'s rows with the whole offset
   // in the lane's voffset: keys at or past T fall outside the descriptor and
   // the hardware drops them, so no store needs a branch or 64-bit address
   // arithmetic.  (A slice of 2^31 bytes or more takes the plain loop below.)
   const int64_t row_elems = (int64_t)a.Hkv * D;  // elements between consecutive keys
-  const int64_t slice0 = (int64_t)b * T * row_elems + (int64_t)kvh * D;
+  const int64_t slice0 = (int64_t)eb * T * row_elems + (int64_t)ekvh * D;
   const int esz = a.grad_bf16 ? 2 : 4;
   const int64_t slice_bytes = ((int64_t)(T - 1) * row_elems + D) * esz;
   if (slice_bytes < ((int64_t)1 << 31)) {
@@ -482,7 +530,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
         xpose(vk);  // all lanes take part in the exchange
         xpose(vv);
         if (d0 >= D) continue;  // whole quads (D is a multiple of 16)
-        const int kk = kw0 + acc_row(4 * j, g) + q;
+        const int kk = ekw0 + acc_row(4 * j, g) + q;
         const int voff = (int)(((int64_t)kk * row_elems + d0) * esz);
         if (a.grad_bf16) {
           auto pack = [](float x, float y) __attribute__((always_inline)) {
@@ -518,17 +566,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
         }
       }
     }
-    return;
-  }
+  } else {
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     const int d = 32 * db + l32;
     if (d < D) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = kw0 + acc_row(r, g);
+        const int kk = ekw0 + acc_row(r, g);
         if (kk < T) {
-          const int64_t off = ((int64_t)b * T + kk) * a.Hkv * D + (int64_t)kvh * D + d;
+          const int64_t off = ((int64_t)eb * T + kk) * a.Hkv * D + (int64_t)ekvh * D + d;
           float vk = dk[db][r] * a.scale, vv = dv[db][r];
           if (a.grad_bf16) {
             bf16* pk = static_cast<bf16*>(a.dK) + off;
@@ -552,6 +599,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
         }
       }
     }
+  }
+  }
+  if (next < n_items && G > 0) publish(0);
+  item = next;
   }
 }
 
@@ -584,6 +635,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   int b, h;
   query_row(it0.row, a.B, a.Hkv, a.group, b, h);
   const int kvh = h / a.group;
+  // Running first (it computes the statistics), this kernel resets the
+  // dK/dV kernel's work counter.
+  if (a.stats && blockIdx.x == 0 && tid == 0) *a.queue = 0;
 
   const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;
   const int64_t qrec = (int64_t)(T - 1) * qpitch + 2 * D;
@@ -809,7 +863,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
 template <int D>
 static hipError_t launch_dkdv_fast_t(const Problem& p, const BwdArgs& a, hipStream_t s) {
   const int n_kt = (p.T + DkdvFastCfg<D>::kBK - 1) / DkdvFastCfg<D>::kBK;
-  const dim3 grid(n_kt * p.Hkv * p.B), block(kThreads);
+  const int n_items = n_kt * p.Hkv * p.B;
+  int cus = 0;
+  const hipError_t ec = device_cus(&cus);
+  if (ec != hipSuccess) return ec;
+  const dim3 grid(n_items < cus ? n_items : cus), block(kThreads);
   const ProfileMark mk = profile_begin(s);
   hipLaunchKernelGGL((attn_bwd_dkdv_fast_kernel<D>), grid, block, 0, s, a);
   const hipError_t e = hipGetLastError();

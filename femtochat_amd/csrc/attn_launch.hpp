@@ -32,6 +32,7 @@ struct PreArgs {
   float* delta;
   float* lse2;
   void* dO16;  // bf16 copy of an fp32 dO (fast mode only), else null
+  int* queue;  // the dK/dV kernel's work counter, reset here; null when not used
   int H, T, B;
   int dO_bf16, O_bf16;
 };
@@ -63,6 +64,9 @@ struct BwdArgs {
   void* dQ;
   void* dK;
   void* dV;
+  // Work counter of the fast dK/dV kernel (workspace): zeroed by the kernel
+  // that runs just before it (the preprocess, or the dQ kernel with stats).
+  int* queue;
   int H, Hkv, T, B, group, left, right;
   int grad_bf16, accumulate;
   float scale;       // 1/sqrt(D)
@@ -149,6 +153,9 @@ struct EmbedSortLayout {
 };
 EmbedSortLayout embed_sort_layout(int64_t N, int vocab);
 hipError_t launch_embed_sorted(const EmbedArgs& a, bool bf16_dy, void* workspace, hipStream_t s);
+
+// Compute units of the current device (cached per device).
+hipError_t device_cus(int* cus);
 
 // Kernel launchers (return the hipError_t of the launch).
 hipError_t launch_fwd(const Problem& p, const FwdArgs& a, hipStream_t s);

@@ -111,9 +111,10 @@ inline fc_status make_problem(const fc_attn_desc* d, Problem* p, char* msg, size
 
 // Workspace layout of the backward pass (byte offsets, 256-aligned): Delta
 // and the base-2 log-sum-exp per query, per-32-query key bounds with
-// positions, and a bf16 copy of an fp32 dO in fast mode.
+// positions, a bf16 copy of an fp32 dO in fast mode, and in fast mode the
+// dK/dV kernel's work counter.
 struct BwdWorkspace {
-  size_t delta, lse2, chunk_lb, dO16, total;
+  size_t delta, lse2, chunk_lb, dO16, queue, total;
 };
 
 inline BwdWorkspace bwd_workspace(const Problem& p) {
@@ -129,6 +130,8 @@ inline BwdWorkspace bwd_workspace(const Problem& p) {
   if (p.positions) off = align(off + (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t));
   w.dO16 = off;
   if (p.bf16 && !p.dout_bf16) off = align(off + nq * p.D * sizeof(uint16_t));
+  w.queue = off;  // the fast dK/dV kernel's work counter
+  if (p.bf16) off = align(off + sizeof(int32_t));
   w.total = off;
   return w;
 }

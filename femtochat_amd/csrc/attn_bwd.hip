@@ -36,7 +36,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_pre_kernel(PreArgs a) {
   const int sub = tid % LPQ;
   const int64_t idx = (int64_t)blockIdx.x * QPB + tid / LPQ;  // (b, t, h) order
   const int64_t n = (int64_t)a.B * a.T * a.H;
-  if (a.queue != nullptr && blockIdx.x == 0 && tid == 0) *a.queue = 0;
+  if (a.queue != nullptr && blockIdx.x == 0 && tid < kXcds) a.queue[tid] = 0;
   float acc = 0.0f;
   if (idx < n) {
     const TD* dO = static_cast<const TD*>(a.dO) + idx * D + 8 * sub;

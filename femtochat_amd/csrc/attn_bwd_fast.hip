@@ -253,10 +253,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   // Work items are (key tile, batch, KV head), key tiles that the most query
   // tiles can see first (item = rank * rows + row).  The grid is one
   // workgroup per CU; each takes item blockIdx.x first and then the next
-  // unclaimed one, gridDim.x + a counter the preceding kernel zeroed, so the
-  // heaviest items go first and every workgroup stays busy to the end.
+  // unclaimed item of its XCD's share (items i with i % 8 equal to the
+  // XCD, blockIdx.x % 8, to which the hardware sends the workgroup), from one
+  // counter per XCD that the preceding kernel zeroed.  So the heaviest items
+  // go first, every workgroup stays busy to the end, and with a multiple of
+  // 8 rows each (batch, KV head) row stays on one XCD, whose L2 then serves
+  // its Q and dO tiles to all its key tiles.
   const int rows = a.Hkv * a.B;
   const int n_items = ((T + C::kBK - 1) / C::kBK) * rows;
+  const int xcd = (int)blockIdx.x % kXcds;
+  const int xcd_first = ((int)gridDim.x - xcd + kXcds - 1) / kXcds;  // items taken first by this XCD's workgroups
 
   // K and V of the wave's 32 keys of an item as B operands (lane = key).
   // The next item's are loaded while this item's dK and dV are stored.
@@ -445,7 +451,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   while (item < n_items) {
   // Claim the next item now; its index is read once this item's steps are done.
   int claimed = 0;
-  if (tid == 0) claimed = (int)gridDim.x + atomicAdd(a.queue, 1);
+  if (tid == 0) claimed = xcd + kXcds * (xcd_first + atomicAdd(a.queue + xcd, 1));
 
 #pragma unroll
   for (int i = 0; i < DB; ++i) {
@@ -636,8 +642,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   query_row(it0.row, a.B, a.Hkv, a.group, b, h);
   const int kvh = h / a.group;
   // Running first (it computes the statistics), this kernel resets the
-  // dK/dV kernel's work counter.
-  if (a.stats && blockIdx.x == 0 && tid == 0) *a.queue = 0;
+  // dK/dV kernel's work counters.
+  if (a.stats && blockIdx.x == 0 && tid < kXcds) a.queue[tid] = 0;
 
   const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;
   const int64_t qrec = (int64_t)(T - 1) * qpitch + 2 * D;
@@ -867,7 +873,9 @@ static hipError_t launch_dkdv_fast_t(const Problem& p, const BwdArgs& a, hipStre
   int cus = 0;
   const hipError_t ec = device_cus(&cus);
   if (ec != hipSuccess) return ec;
-  const dim3 grid(n_items < cus ? n_items : cus), block(kThreads);
+  // Every XCD needs a workgroup unless every item has its own.
+  const int slots = cus >= kXcds && cus < n_items ? cus : n_items;
+  const dim3 grid(slots), block(kThreads);
   const ProfileMark mk = profile_begin(s);
   hipLaunchKernelGGL((attn_bwd_dkdv_fast_kernel<D>), grid, block, 0, s, a);
   const hipError_t e = hipGetLastError();

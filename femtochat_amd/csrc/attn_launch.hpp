@@ -32,7 +32,7 @@ struct PreArgs {
   float* delta;
   float* lse2;
   void* dO16;  // bf16 copy of an fp32 dO (fast mode only), else null
-  int* queue;  // the dK/dV kernel's work counter, reset here; null when not used
+  int* queue;  // the dK/dV kernel's work counters (kXcds), reset here; null when not used
   int H, T, B;
   int dO_bf16, O_bf16;
 };
@@ -64,8 +64,9 @@ struct BwdArgs {
   void* dQ;
   void* dK;
   void* dV;
-  // Work counter of the fast dK/dV kernel (workspace): zeroed by the kernel
-  // that runs just before it (the preprocess, or the dQ kernel with stats).
+  // Work counters of the fast dK/dV kernel (workspace, one per XCD): zeroed
+  // by the kernel that runs just before it (the preprocess, or the dQ
+  // kernel with stats).
   int* queue;
   int H, Hkv, T, B, group, left, right;
   int grad_bf16, accumulate;

@@ -26,6 +26,9 @@ struct Problem {
   bool positions;
 };
 
+// XCDs of an MI355X: the hardware sends workgroup id to XCD id % kXcds.
+constexpr int kXcds = 8;
+
 // Head dims the kernels are compiled for.
 inline bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
@@ -130,8 +133,8 @@ inline BwdWorkspace bwd_workspace(const Problem& p) {
   if (p.positions) off = align(off + (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t));
   w.dO16 = off;
   if (p.bf16 && !p.dout_bf16) off = align(off + nq * p.D * sizeof(uint16_t));
-  w.queue = off;  // the fast dK/dV kernel's work counter
-  if (p.bf16) off = align(off + sizeof(int32_t));
+  w.queue = off;  // the fast dK/dV kernel's work counters, one per XCD
+  if (p.bf16) off = align(off + kXcds * sizeof(int32_t));
   w.total = off;
   return w;
 }

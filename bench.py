@@ -332,7 +332,8 @@ def measure_attention(wl, dev, steps: int, warmup: int) -> dict:
     import torch
 
     import femtochat_amd._lib as L
-    from femtochat_amd import MFMAExact, MFMAFast, attention_, backward_workspace_bytes, delta_attention_
+    from femtochat_amd import (MFMAExact, MFMAFast, attention_, backward_workspace_bytes, delta_attention_,
+                               forward_workspace_bytes)
     from femtochat_amd import workloads as W
 
     fast = wl.mode == "fast"
@@ -346,13 +347,15 @@ def measure_attention(wl, dev, steps: int, warmup: int) -> dict:
         m = torch.empty((wl.B, wl.H, wl.T), device=dev)
         dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
         ws = torch.empty(backward_workspace_bytes(A, Q, K, positions=pos), dtype=torch.uint8, device=dev)
+        nf = forward_workspace_bytes(A, Q, K, positions=pos)
+        fws = torch.empty(nf, dtype=torch.uint8, device=dev) if nf > 0 else None
         pairs = W.visible_pairs(wl.T, wl.B, wl.H, window, None if pos is None else pos.cpu().numpy())
         total_pairs += pairs
-        layers.append((Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws))
+        layers.append((Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws, fws))
 
     def step():
-        for (Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws) in layers:
-            attention_(A, O, l, m, Q, K, V, window, positions=pos)
+        for (Q, K, V, dO, pos, window, O, l, m, dQ, dK, dV, ws, fws) in layers:
+            attention_(A, O, l, m, Q, K, V, window, positions=pos, workspace=fws)
             delta_attention_(A, dQ, dK, dV, dO, Q, K, V, O, l, m, window, positions=pos, accumulate=False,
                              workspace=ws)
 

@@ -20,6 +20,7 @@ from .kernels import (  # noqa: F401
     attention_inputs,
     attention_state,
     backward_workspace_bytes,
+    forward_workspace_bytes,
     capabilities,
     convert_,
     delta_attention_,

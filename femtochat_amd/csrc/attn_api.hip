@@ -143,7 +143,7 @@ fc_status fc_attn_workspace_bytes(const fc_attn_desc* desc, int32_t pass, int32_
   if (bytes == nullptr) return fail(FC_ERR_INVALID_ARGUMENT, "bytes is null");
   p.positions = positions_given != 0;
   if (pass == FC_PASS_FORWARD) {
-    *bytes = 0;
+    *bytes = fc::fwd_workspace(p).total;
   } else if (pass == FC_PASS_BACKWARD) {
     *bytes = fc::bwd_workspace(p).total;
   } else {
@@ -155,19 +155,36 @@ fc_status fc_attn_workspace_bytes(const fc_attn_desc* desc, int32_t pass, int32_
 fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, const void* V,
                       const int32_t* positions, void* O, float* l, float* m, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   fc::Problem p;
   fc_status st = make_problem(desc, &p);
   if (st != FC_OK) return st;
   if (Q == nullptr || K == nullptr || V == nullptr || O == nullptr || l == nullptr || m == nullptr)
     return fail(FC_ERR_INVALID_ARGUMENT, "fc_attn_fwd: a required pointer is null");
   p.positions = positions != nullptr;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // The workspace is optional: with one, fast mode with positions takes the
+  // query tiles in the work order.
+  const fc::FwdWorkspace ws = fc::fwd_workspace(p);
+  int32_t* order = nullptr;
+  if (ws.total > 0 && workspace != nullptr) {
+    if (workspace_bytes < ws.total)
+      return fail(FC_ERR_WORKSPACE, "forward workspace needs %zu bytes, got %zu", ws.total, workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+      return fail(FC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    char* w = static_cast<char*>(workspace);
+    int32_t* chunk_lb = reinterpret_cast<int32_t*>(w + ws.chunk_lb);
+    order = reinterpret_cast<int32_t*>(w + ws.qorder);
+    hipError_t e = fc::launch_bounds(p, fc::BoundsArgs{positions, chunk_lb, p.T, p.B, p.left}, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "bounds launch failed: %s", hipGetErrorString(e));
+    e = fc::launch_order(p, fc::OrderArgs{chunk_lb, order, nullptr, p.T, p.B, p.left, p.right}, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "order launch failed: %s", hipGetErrorString(e));
+  }
   fc::FwdArgs a{};
   a.Q = Q;
   a.K = K;
   a.V = V;
   a.pos = positions;
+  a.order = order;
   a.O = O;
   a.l = l;
   a.m = m;
@@ -180,7 +197,7 @@ fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, co
   a.right = p.right;
   a.out_bf16 = p.out_bf16 ? 1 : 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)p.D));
-  const hipError_t e = fc::launch_fwd(p, a, static_cast<hipStream_t>(stream));
+  const hipError_t e = fc::launch_fwd(p, a, s);
   if (e != hipSuccess) return fail(FC_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
@@ -243,6 +260,14 @@ fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const 
     e = fc::launch_bounds(p, ba, s);
     if (e != hipSuccess) return fail(FC_ERR_HIP, "bounds launch failed: %s", hipGetErrorString(e));
   }
+  int32_t* qorder = nullptr;
+  int32_t* korder = nullptr;
+  if (fc::ordered(p)) {
+    qorder = reinterpret_cast<int32_t*>(w + ws.qorder);
+    korder = reinterpret_cast<int32_t*>(w + ws.korder);
+    e = fc::launch_order(p, fc::OrderArgs{chunk_lb, qorder, korder, p.T, p.B, p.left, p.right}, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "order launch failed: %s", hipGetErrorString(e));
+  }
 
   fc::BwdArgs a{};
   a.dO = pa.dO16 != nullptr ? pa.dO16 : dO;
@@ -253,6 +278,8 @@ fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const 
   a.lse2 = pa.lse2;
   a.pos = positions;
   a.chunk_lb = chunk_lb;
+  a.qorder = qorder;
+  a.korder = korder;
   a.queue = queue;
   a.dQ = dQ;
   a.dK = dK;

@@ -65,21 +65,115 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_pre_kernel(PreArgs a) {
   }
 }
 
-// Per 32-query chunk (min, max) of the document-aware key lower bound.
+// Per 32-query chunk (min, max) of the document-aware key lower bound (a
+// query at or beyond T counts as T).  One lane per query, so a half-wave
+// reads one chunk's 32 positions in one coalesced access and reduces them.
 __global__ __launch_bounds__(kThreads) void attn_bounds_kernel(BoundsArgs a) {
   const int nc = (a.T + 31) / 32;
-  const int i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= nc * a.B) return;
-  const int b = i / nc, c = i - b * nc;
-  const int32_t* pos = a.pos + (int64_t)b * a.T;
-  int lo = a.T, hi = 0;
-  for (int q = 32 * c; q < 32 * c + 32; ++q) {
-    const int lb = key_lb(q, a.T, a.left, pos);
-    lo = min(lo, lb);
-    hi = max(hi, lb);
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t chunk = i >> 5;
+  const bool live = chunk < (int64_t)nc * a.B;  // uniform over each half-wave
+  const int b = live ? (int)(chunk / nc) : 0;
+  const int q = live ? 32 * (int)(chunk - (int64_t)b * nc) + (int)(i & 31) : a.T;
+  const int lb = key_lb(q, a.T, a.left, a.pos + (int64_t)b * a.T);
+  const int lo = wave_min32(lb), hi = wave_max32(lb);
+  if (live && (i & 31) == 0) {
+    a.chunk_lb[2 * chunk] = lo;
+    a.chunk_lb[2 * chunk + 1] = hi;
   }
-  a.chunk_lb[2 * i] = lo;
-  a.chunk_lb[2 * i + 1] = hi;
+}
+
+// Work order of the fast kernels' tiles with positions, in one workgroup.
+// The smallest key lower bound of every 128-query tile (from the chunk
+// bounds) goes to LDS; then the work of each item of 128 rows, in steps:
+//  * query tile [q0, q1] (forward and dQ): the 64-key tiles from the one
+//    holding its smallest lower bound up to the one holding key_ub(q1);
+//  * key tile [k0, k1] (dK/dV): the 128-query tiles between k0 - right and
+//    k1 + left whose smallest lower bound is at most k1, which are the
+//    tiles the dK/dV kernel visits;
+// and finally each item's rank: the items of more work, plus the items of
+// equal work and lower index.  order[rank] = item.  The inner loops read
+// LDS in runs of 8 with no exit inside a run, so the reads of a run are in
+// flight together.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderRun = 8;
+
+__global__ __launch_bounds__(kOrderThreads) void attn_order_kernel(OrderArgs a) {
+  static_assert(kOrderKStep == kOrderRows, "a dK/dV step is one tabulated query tile");
+  __shared__ int s_lb[kOrderMaxItems + kOrderRun];
+  __shared__ __attribute__((aligned(16))) int s_work[kOrderMaxItems + kOrderRun];
+  const int tid = threadIdx.x, T = a.T;
+  const int nc = (T + 31) / 32, n128 = (T + kOrderRows - 1) / kOrderRows;
+  const int items = a.B * n128;
+  constexpr int kChunks = kOrderRows / 32;
+  for (int i = tid; i < items; i += kOrderThreads) {
+    const int b = i / n128, t = i - b * n128;
+    const int32_t* cb = a.chunk_lb + (int64_t)b * nc * 2;
+    int lo = T;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) lo = min(lo, cb[2 * min(kChunks * t + c, nc - 1)]);  // loads without a branch
+    s_lb[i] = lo;
+  }
+  // Padding after the last item: never counted (ranks) or masked (key steps).
+  if (tid < kOrderRun) s_work[items + tid] = INT_MIN;
+
+  // sub lanes (a power of two up to a wave) count one item's rank together,
+  // each over every sub-th run of kOrderRun items, and add their counts
+  // with shuffles.
+  int sub = 1;
+  while (sub < kWave && sub * 2 * items <= kOrderThreads) sub *= 2;
+  const int per = kOrderThreads / sub, part = tid & (sub - 1);
+  auto rank_into = [&](int32_t* order) {
+    for (int i0 = 0; i0 < items; i0 += per) {  // the same trip count on every lane
+      const int i = i0 + tid / sub;
+      const bool live = i < items;
+      const int w = s_work[live ? i : 0];
+      int r = 0;
+      for (int j0 = kOrderRun * part; j0 < items; j0 += kOrderRun * sub) {
+        int v[kOrderRun];
+#pragma unroll
+        for (int e = 0; e < kOrderRun; ++e) v[e] = s_work[j0 + e];
+#pragma unroll
+        for (int e = 0; e < kOrderRun; ++e) r += (v[e] > w || (v[e] == w && j0 + e < i)) ? 1 : 0;
+      }
+      for (int o = 1; o < sub; o <<= 1) r += __shfl_xor(r, o);
+      if (live && part == 0) order[r] = i;
+    }
+  };
+  __syncthreads();
+  if (a.qorder != nullptr) {
+    for (int i = tid; i < items; i += kOrderThreads) {
+      const int t = i % n128;
+      const int kmin = s_lb[i];
+      const int kmax = key_ub(min(t * kOrderRows + kOrderRows - 1, T - 1), T, a.right);
+      s_work[i] = kmax >= kmin ? (kmax - (kmin / kOrderTile) * kOrderTile) / kOrderTile + 1 : 0;
+    }
+    __syncthreads();
+    rank_into(a.qorder);
+    __syncthreads();
+  }
+  if (a.korder != nullptr) {
+    for (int i = tid; i < items; i += kOrderThreads) {
+      const int b = i / n128, t = i - b * n128;
+      const int k0 = t * kOrderRows, k1 = min(k0 + kOrderRows, T) - 1;
+      const int qlo = max(0, k0 - a.right), qhi = min(T - 1, k1 + a.left);
+      int n = 0;
+      if (qhi >= qlo) {
+        const int* row = s_lb + b * n128;
+        const int ulast = qhi / kOrderKStep;
+        for (int u0 = qlo / kOrderKStep; u0 <= ulast; u0 += kOrderRun) {
+          int v[kOrderRun];
+#pragma unroll
+          for (int e = 0; e < kOrderRun; ++e) v[e] = row[u0 + e];  // within the padded table
+#pragma unroll
+          for (int e = 0; e < kOrderRun; ++e) n += (u0 + e <= ulast && v[e] <= k1) ? 1 : 0;
+        }
+      }
+      s_work[i] = n;
+    }
+    __syncthreads();
+    rank_into(a.korder);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -528,12 +622,21 @@ hipError_t launch_bwd_pre(const Problem& p, const PreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_bounds(const Problem& p, const BoundsArgs& a, hipStream_t s) {
-  const int n = ((p.T + 31) / 32) * p.B;
-  const dim3 grid((n + kThreads - 1) / kThreads), block(kThreads);
+  const int64_t n = (int64_t)((p.T + 31) / 32) * p.B * 32;  // one lane per query slot
+  const dim3 grid((unsigned)((n + kThreads - 1) / kThreads)), block(kThreads);
   const ProfileMark mk = profile_begin(s);
   hipLaunchKernelGGL(attn_bounds_kernel, grid, block, 0, s, a);
   const hipError_t e = hipGetLastError();
   profile_end(mk, "attn_bounds", s);
+  return e;
+}
+
+hipError_t launch_order(const Problem& p, const OrderArgs& a, hipStream_t s) {
+  if (!order_fits(p.T, p.B)) return hipErrorInvalidValue;
+  const ProfileMark mk = profile_begin(s);
+  hipLaunchKernelGGL(attn_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, a);
+  const hipError_t e = hipGetLastError();
+  profile_end(mk, "attn_order", s);
   return e;
 }
 

@@ -260,16 +260,35 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   // 8 rows each (batch, KV head) row stays on one XCD, whose L2 then serves
   // its Q and dO tiles to all its key tiles.
   const int rows = a.Hkv * a.B;
-  const int n_items = ((T + C::kBK - 1) / C::kBK) * rows;
+  const int n_kt = (T + C::kBK - 1) / C::kBK;
+  const int n_items = n_kt * rows;
   const int xcd = (int)blockIdx.x % kXcds;
+  static_assert(C::kBK == kOrderRows && C::kBQ == kOrderKStep, "the work order counts this tiling");
+  // (batch, KV head, key tile) of an item: in the work order (korder[k] =
+  // b * n_kt + kt names the k-th key tile, whose Hkv KV heads are
+  // consecutive items), else key tiles outer and rows inner.
+  auto decode = [&](int item, int& ib, int& ikvh, int& ikt) {
+    if (a.korder != nullptr) {
+      const int k = item / a.Hkv;
+      ikvh = item - k * a.Hkv;
+      const int e = a.korder[k];
+      ib = e / n_kt;
+      ikt = e - ib * n_kt;
+    } else {
+      const int row = item % rows;
+      ikt = item / rows;
+      ib = row / a.Hkv;
+      ikvh = row - ib * a.Hkv;
+    }
+  };
   const int xcd_first = ((int)gridDim.x - xcd + kXcds - 1) / kXcds;  // items taken first by this XCD's workgroups
 
   // K and V of the wave's 32 keys of an item as B operands (lane = key).
   // The next item's are loaded while this item's dK and dV are stored.
   bf16x8 kf[KC], vf[KC];
   auto load_kv = [&](int item) {
-    const int row = item % rows, ikt = item / rows;
-    const int ib = row / a.Hkv, ikvh = row - ib * a.Hkv;
+    int ib, ikvh, ikt;
+    decode(item, ib, ikvh, ikt);
     const int64_t base = (((int64_t)ib * T * a.Hkv + ikvh) * D) * 2;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(static_cast<const char*>(a.K) + base, (uint32_t)krec);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(static_cast<const char*>(a.V) + base, (uint32_t)krec);
@@ -319,9 +338,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   };
   // Decodes an item and tabulates its tile visibility (ends with a barrier).
   auto setup = [&](int it) {
-    const int kt = it / rows;
-    b = (it % rows) / a.Hkv;
-    kvh = (it % rows) - b * a.Hkv;
+    int kt;
+    decode(it, b, kvh, kt);
     k0 = kt * C::kBK;
     k1 = min(k0 + C::kBK, T) - 1;
     kw0 = k0 + 32 * wave;
@@ -636,10 +654,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_qt = (T + C::kBM - 1) / C::kBM;
-  const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
-  const int qt = n_qt - 1 - it0.rank;  // longest query tiles first
-  int b, h;
-  query_row(it0.row, a.B, a.Hkv, a.group, b, h);
+  static_assert(C::kBM == kOrderRows && C::kBN == kOrderTile, "the work order counts this tiling");
+  int b, h, qt;
+  if (a.qorder != nullptr) {
+    ordered_query_item(blockIdx.x, a.qorder, n_qt, a.H, a.Hkv, a.group, b, h, qt);
+  } else {
+    const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
+    qt = n_qt - 1 - it0.rank;  // longest query tiles first
+    query_row(it0.row, a.B, a.Hkv, a.group, b, h);
+  }
   const int kvh = h / a.group;
   // Running first (it computes the statistics), this kernel resets the
   // dK/dV kernel's work counters.

@@ -162,6 +162,20 @@ __device__ inline void query_row(int r, int B, int Hkv, int group, int& b, int& 
   h = (bkv - b * Hkv) * group + gi;
 }
 
+// (batch, query head, query tile) of item id of a query-tile grid taken in a
+// work order: order[k] = b * n_tiles + tile names the k-th tile, whose H
+// heads are the ids k*H .. k*H + H-1, numbered like query_row's rows of one
+// batch row (so the heads that share a KV head are Hkv ids apart).
+__device__ inline void ordered_query_item(int id, const int32_t* order, int n_tiles, int H, int Hkv, int group,
+                                          int& b, int& h, int& tile) {
+  const int k = id / H, hi = id - k * H;
+  const int e = order[k];
+  b = e / n_tiles;
+  tile = e - b * n_tiles;
+  int b0;
+  query_row(hi, 1, Hkv, group, b0, h);
+}
+
 // Visible key range of query q (0-based): lb <= k <= ub.  left/right are the
 // normalised window (causal -> left = T); pos is the row's positions or null.
 __device__ inline int key_lb(int q, int T, int left, const int32_t* pos) {

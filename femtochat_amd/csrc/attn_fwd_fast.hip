@@ -93,10 +93,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
   const int g = lane >> 5, l32 = lane & 31;
   const int T = a.T;
   const int n_qt = (T + C::kBM - 1) / C::kBM;
-  const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
-  const int qt = n_qt - 1 - it0.rank;  // longest query tiles first
-  int b, h;
-  query_row(it0.row, a.B, a.Hkv, a.group, b, h);
+  static_assert(C::kBM == kOrderRows && C::kBN == kOrderTile, "the work order counts this tiling");
+  int b, h, qt;
+  if (a.order != nullptr) {
+    ordered_query_item(blockIdx.x, a.order, n_qt, a.H, a.Hkv, a.group, b, h, qt);
+  } else {
+    const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
+    qt = n_qt - 1 - it0.rank;  // longest query tiles first
+    query_row(it0.row, a.B, a.Hkv, a.group, b, h);
+  }
   const int kvh = h / a.group;
 
   const int qpitch = a.H * D * 2, kpitch = a.Hkv * D * 2;  // bytes between tokens

@@ -16,6 +16,7 @@ struct FwdArgs {
   const void* K;
   const void* V;
   const int32_t* pos;
+  const int32_t* order;  // fast mode with positions: query tiles in work order, or null
   void* O;
   float* l;
   float* m;
@@ -43,6 +44,14 @@ struct BoundsArgs {
   int T, B, left;
 };
 
+// Work order of the fast kernels with positions: attn_problem.hpp.
+struct OrderArgs {
+  const int32_t* chunk_lb;  // the bounds kernel's output
+  int32_t* qorder;          // query tiles by decreasing key tiles, or null
+  int32_t* korder;          // key tiles by decreasing query steps, or null
+  int T, B, left, right;
+};
+
 struct BwdArgs {
   const void* dO;  // in the input element type (bf16 copy when needed)
   const void* Q;
@@ -61,6 +70,8 @@ struct BwdArgs {
   float* lse2_out;
   const int32_t* pos;
   const int32_t* chunk_lb;
+  const int32_t* qorder;  // fast mode with positions: dQ tiles in work order, or null
+  const int32_t* korder;  // and the dK/dV kernel's key tiles, or null
   void* dQ;
   void* dK;
   void* dV;
@@ -162,6 +173,7 @@ hipError_t device_cus(int* cus);
 hipError_t launch_fwd(const Problem& p, const FwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_pre(const Problem& p, const PreArgs& a, hipStream_t s);
 hipError_t launch_bounds(const Problem& p, const BoundsArgs& a, hipStream_t s);
+hipError_t launch_order(const Problem& p, const OrderArgs& a, hipStream_t s);
 hipError_t launch_bwd_dkdv(const Problem& p, const BwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_dq(const Problem& p, const BwdArgs& a, hipStream_t s);
 // Fast-mode (bf16) kernels, attn_fwd_fast.hip / attn_bwd_fast.hip.

@@ -29,6 +29,23 @@ struct Problem {
 // XCDs of an MI355X: the hardware sends workgroup id to XCD id % kXcds.
 constexpr int kXcds = 8;
 
+// Work order of the fast kernels with positions (attn_order_kernel in
+// attn_bwd.hip): the tiles of all batch rows sorted by decreasing work, ties
+// by index, so that the tiles of long documents start first.  The work is counted for the
+// tilings below (fast forward and dQ: 128 queries per workgroup against
+// 64-key tiles; fast dK/dV: 128 keys per item against 128-query steps); the
+// kernels assert that they use them.  An order entry is b * n + tile with
+// n = ceil(T / 128).
+constexpr int kOrderRows = 128;         // queries (keys) per forward and dQ (dK/dV) item
+constexpr int kOrderTile = 64;          // keys per step of a forward or dQ item
+constexpr int kOrderKStep = 128;        // queries per step of a dK/dV item
+constexpr int kOrderMaxItems = 4096;    // largest B * ceil(T / 128) the order kernel tabulates
+inline bool order_fits(int T, int B) { return (int64_t)B * ((T + kOrderRows - 1) / kOrderRows) <= kOrderMaxItems; }
+
+// Fast mode with positions takes the tiles in the work order when the order
+// kernel's tables fit.
+inline bool ordered(const Problem& p) { return p.bf16 && p.positions && order_fits(p.T, p.B); }
+
 // Head dims the kernels are compiled for.
 inline bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
@@ -112,29 +129,57 @@ inline fc_status make_problem(const fc_attn_desc* d, Problem* p, char* msg, size
   return FC_OK;
 }
 
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+inline size_t chunk_bounds_bytes(const Problem& p) { return (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t); }
+inline size_t order_bytes(const Problem& p) { return (size_t)p.B * ((p.T + kOrderRows - 1) / kOrderRows) * sizeof(int32_t); }
+
+// Workspace layout of the forward pass (byte offsets, 256-aligned): empty
+// unless the work order applies, then the per-32-query key bounds and the
+// query tiles' order.  The forward runs without it too (default order).
+struct FwdWorkspace {
+  size_t chunk_lb, qorder, total;
+};
+
+inline FwdWorkspace fwd_workspace(const Problem& p) {
+  FwdWorkspace w{};
+  size_t off = 0;
+  if (ordered(p)) {
+    w.chunk_lb = off;
+    off = align256(off + chunk_bounds_bytes(p));
+    w.qorder = off;
+    off = align256(off + order_bytes(p));
+  }
+  w.total = off;
+  return w;
+}
+
 // Workspace layout of the backward pass (byte offsets, 256-aligned): Delta
 // and the base-2 log-sum-exp per query, per-32-query key bounds with
-// positions, a bf16 copy of an fp32 dO in fast mode, and in fast mode the
-// dK/dV kernel's work counter.
+// positions, a bf16 copy of an fp32 dO in fast mode, in fast mode the
+// dK/dV kernel's work counters, and the dQ and dK/dV orders when the work
+// order applies.
 struct BwdWorkspace {
-  size_t delta, lse2, chunk_lb, dO16, queue, total;
+  size_t delta, lse2, chunk_lb, dO16, queue, qorder, korder, total;
 };
 
 inline BwdWorkspace bwd_workspace(const Problem& p) {
-  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   BwdWorkspace w{};
   const size_t nq = (size_t)p.B * p.H * p.T;
   size_t off = 0;
   w.delta = off;
-  off = align(off + nq * sizeof(float));
+  off = align256(off + nq * sizeof(float));
   w.lse2 = off;
-  off = align(off + nq * sizeof(float));
+  off = align256(off + nq * sizeof(float));
   w.chunk_lb = off;
-  if (p.positions) off = align(off + (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t));
+  if (p.positions) off = align256(off + chunk_bounds_bytes(p));
   w.dO16 = off;
-  if (p.bf16 && !p.dout_bf16) off = align(off + nq * p.D * sizeof(uint16_t));
+  if (p.bf16 && !p.dout_bf16) off = align256(off + nq * p.D * sizeof(uint16_t));
   w.queue = off;  // the fast dK/dV kernel's work counters, one per XCD
-  if (p.bf16) off = align(off + kXcds * sizeof(int32_t));
+  if (p.bf16) off = align256(off + kXcds * sizeof(int32_t));
+  w.qorder = off;
+  if (ordered(p)) off = align256(off + order_bytes(p));
+  w.korder = off;
+  if (ordered(p)) off = align256(off + order_bytes(p));
   w.total = off;
   return w;
 }

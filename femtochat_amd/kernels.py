@@ -49,6 +49,7 @@ __all__ = [
     "attention_",
     "delta_attention_",
     "backward_workspace_bytes",
+    "forward_workspace_bytes",
     "attention_state",
     "accumulator_type",
     "attention_inputs",
@@ -270,10 +271,14 @@ def _check_common(A, Q, K, V, positions):
     return device, B, T, H, Hkv, D
 
 
-def attention_(A, O, l, m, Q, K, V, window: Tuple[int, int], *, positions=None, **options) -> None:
+def attention_(A, O, l, m, Q, K, V, window: Tuple[int, int], *, positions=None,
+               workspace: Optional[torch.Tensor] = None, **options) -> None:
     """Forward into caller buffers: ``attention!(𝒜, O, ℓ, m, Q, K, V, window)``
     (src/kernels.jl:419; ext/FemtoChatCUDAExt.jl:1242-1260).  O is bfloat16 or
-    float32 (fast) / float32 (exact); ℓ and m are float32 (B,H,T)."""
+    float32 (fast) / float32 (exact); ℓ and m are float32 (B,H,T).  With
+    positions in fast mode the library orders the query tiles by their work
+    in a small workspace (allocated here unless ``workspace`` is given, of
+    ``forward_workspace_bytes`` bytes); other problems need none."""
     _reject_unknown(options)
     device, B, T, H, Hkv, D = _check_common(A, Q, K, V, positions)
     out_dtypes = (torch.bfloat16, torch.float32) if isinstance(A, MFMAFast) else (torch.float32,)
@@ -283,10 +288,22 @@ def attention_(A, O, l, m, Q, K, V, window: Tuple[int, int], *, positions=None, 
     oc = _dtype_code(O.dtype)
     d = _desc(A, Q, K, window, oc, oc, oc)
     lib = _lib.lib()
+    nbytes = ctypes.c_size_t(0)
+    _lib.check(lib.fc_attn_workspace_bytes(ctypes.byref(d), _lib.FC_PASS_FORWARD, int(positions is not None),
+                                           ctypes.byref(nbytes)))
+    ws, aligned = None, None
+    if nbytes.value > 0:
+        if workspace is None:
+            ws = torch.empty(int(nbytes.value) + 256, dtype=torch.uint8, device=device)
+        else:
+            ws = workspace
+            if ws.device != device or ws.numel() * ws.element_size() < int(nbytes.value) + 256:
+                raise ValueError(f"workspace must be a {int(nbytes.value) + 256}-byte tensor on {device}")
+        aligned = ctypes.c_void_p((ws.data_ptr() + 255) & ~255)
     _lib.check(
         lib.fc_attn_fwd(
             ctypes.byref(d), _ptr(Q), _ptr(K), _ptr(V), _ptr(positions), _ptr(O), _ptr(l), _ptr(m),
-            None, 0, _stream_ptr(device),
+            aligned, ctypes.c_size_t(int(nbytes.value) if ws is not None else 0), _stream_ptr(device),
         )
     )
 
@@ -334,6 +351,17 @@ def delta_attention_(
     # An internally allocated workspace must outlive the kernels on this stream.
     if workspace is None:
         ws.record_stream(torch.cuda.current_stream(device))
+
+
+def forward_workspace_bytes(A, Q, K, *, positions=None) -> int:
+    """Bytes of the caller-owned workspace ``attention_(…, workspace=)``
+    accepts (the library's requirement plus 256 bytes of alignment slack; 0
+    when the problem needs none)."""
+    d = _desc(A, Q, K, (-1, 0), _dtype_code(Q.dtype), _dtype_code(Q.dtype), _dtype_code(Q.dtype))
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fc_attn_workspace_bytes(ctypes.byref(d), _lib.FC_PASS_FORWARD,
+                                                  int(positions is not None), ctypes.byref(n)))
+    return int(n.value) + 256 if n.value > 0 else 0
 
 
 def backward_workspace_bytes(A, Q, K, *, positions=None, dout_dtype=None) -> int:

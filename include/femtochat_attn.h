@@ -89,7 +89,11 @@ fc_status fc_attn_workspace_bytes(const fc_attn_desc* desc, int32_t pass,
 /* Forward: writes O, l, m.  Replaces
    `attention!(𝒜, O, ℓ, m, Q, K, V, window)` (reference src/kernels.jl:419,
    CPU body :131-219; CUDA ext/FemtoChatCUDAExt.jl:1242-1260).
-   positions may be NULL (reference semantics, no document mask). */
+   positions may be NULL (reference semantics, no document mask).
+   The workspace is optional (NULL and 0 are accepted): in fast mode with
+   positions, a workspace of fc_attn_workspace_bytes(FC_PASS_FORWARD) bytes,
+   256-byte aligned, lets the kernel take the query tiles in order of
+   decreasing work (long documents first); the results are the same. */
 fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K,
                       const void* V, const int32_t* positions, void* O,
                       float* l, float* m, void* workspace,

@@ -131,6 +131,43 @@ def test_workspace_checks():
     assert st == L.FC_ERR_WORKSPACE and "aligned" in lib.fc_last_error().decode()
 
 
+def test_forward_workspace_for_the_work_order():
+    """Only fast mode with positions has a forward workspace (chunk bounds and
+    the query-tile order), and only while the order tables fit (B * ceil(T/128)
+    <= 4096); the backward then holds the dQ and dK/dV orders as well."""
+    lib = L.lib()
+
+    def fwd_bytes(d, pos):
+        st, n = ws_bytes(d, L.FC_PASS_FORWARD, pos=pos)
+        assert st == L.FC_OK
+        return n
+
+    d = desc(T=1000, B=3)
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    chunk = align(3 * 32 * 2 * 4)  # ceil(1000/32) = 32 chunks of (min, max)
+    order = align(3 * 8 * 4)       # ceil(1000/128) = 8 tiles per row
+    assert fwd_bytes(d, 0) == 0
+    assert fwd_bytes(d, 1) == chunk + order
+    exact = desc(T=1000, B=3, mode=L.FC_MODE_EXACT, in_dtype=L.FC_F32, out_dtype=L.FC_F32, dout_dtype=L.FC_F32,
+                 grad_dtype=L.FC_F32)
+    assert fwd_bytes(exact, 1) == 0
+    assert fwd_bytes(desc(T=64 * 8192, B=1, H=1, Hkv=1, D=16), 1) > 0
+    assert fwd_bytes(desc(T=64 * 8192 + 1, B=1, H=1, Hkv=1, D=16), 1) == 0
+    _, bwd_pos = ws_bytes(d, pos=1)
+    _, bwd_exact = ws_bytes(exact, pos=1)
+    assert bwd_pos >= 2 * 4 * 3 * 4 * 1000 + chunk + 2 * order
+    # A workspace is optional for the forward, but a short or misaligned one is an error.
+    fake = ctypes.c_void_p(0x1000)
+    need = fwd_bytes(d, 1)
+    st = lib.fc_attn_fwd(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, fake, need - 1, None)
+    assert st == L.FC_ERR_WORKSPACE and str(need) in lib.fc_last_error().decode()
+    st = lib.fc_attn_fwd(ctypes.byref(d), fake, fake, fake, fake, fake, fake, fake, ctypes.c_void_p(0x1001), need,
+                         None)
+    assert st == L.FC_ERR_WORKSPACE and "aligned" in lib.fc_last_error().decode()
+    # Exact mode: Delta, lse2 and the chunk bounds, no work counters or orders.
+    assert bwd_exact == 2 * align(4 * 3 * 4 * 1000) + chunk
+
+
 def test_noalloc_backward_rejects_problems_beyond_its_scratch():
     # Checked on the host before any HIP call: B*H*T = 2^23 query rows need
     # 2 * 4 * 2^23 bytes = 64 MiB of statistics, above the 32 MiB scratch.

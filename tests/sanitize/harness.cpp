@@ -82,6 +82,24 @@ static void validation() {
   const fc::BwdWorkspace c = fc::bwd_workspace(p);
   CHECK(a.total % 256 == 0 && b.total > a.total && c.total >= b.total + 2ull * 3 * 4 * 1000 * 128);
   CHECK(a.delta % 256 == 0 && a.lse2 % 256 == 0 && b.chunk_lb % 256 == 0 && c.dO16 % 256 == 0);
+  // The regions of the ordered backward (fast mode, positions) follow each
+  // other without overlap and end at total; the forward's workspace holds
+  // only the chunk bounds and the query order, and only in that case.
+  const size_t nchunk = 3 * 32 * 2 * 4, norder = 3 * 8 * 4;  // ceil(1000/32) chunks, ceil(1000/128) tiles
+  CHECK(fc::ordered(p));
+  CHECK(c.lse2 >= c.delta + 4ull * 3 * 4 * 1000 && c.chunk_lb >= c.lse2 + 4ull * 3 * 4 * 1000);
+  CHECK(c.dO16 >= c.chunk_lb + nchunk && c.queue >= c.dO16 + 2ull * 3 * 4 * 1000 * 128);
+  CHECK(c.qorder >= c.queue + fc::kXcds * 4 && c.korder >= c.qorder + norder && c.total >= c.korder + norder);
+  CHECK(c.qorder % 256 == 0 && c.korder % 256 == 0 && c.total % 256 == 0);
+  const fc::FwdWorkspace f = fc::fwd_workspace(p);
+  CHECK(f.chunk_lb == 0 && f.qorder >= nchunk && f.qorder % 256 == 0 && f.total >= f.qorder + norder);
+  p.positions = false;
+  CHECK(fc::fwd_workspace(p).total == 0 && !fc::ordered(p));
+  p.positions = true;
+  p.T = 128 * 4096, p.B = 1;
+  CHECK(fc::ordered(p) && fc::order_fits(p.T, p.B));
+  p.T += 1;
+  CHECK(!fc::ordered(p) && fc::fwd_workspace(p).total == 0);
 }
 
 // float64 softmax attention, one (batch, head), for the comparison.

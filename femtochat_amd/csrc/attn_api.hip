@@ -185,6 +185,7 @@ fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, co
   a.V = V;
   a.pos = positions;
   a.order = order;
+  a.local_order = fc::windowed(p) ? 1 : 0;
   a.O = O;
   a.l = l;
   a.m = m;
@@ -280,6 +281,7 @@ fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const 
   a.chunk_lb = chunk_lb;
   a.qorder = qorder;
   a.korder = korder;
+  a.local_order = fc::windowed(p) ? 1 : 0;
   a.queue = queue;
   a.dQ = dQ;
   a.dK = dK;

@@ -266,7 +266,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   static_assert(C::kBK == kOrderRows && C::kBQ == kOrderKStep, "the work order counts this tiling");
   // (batch, KV head, key tile) of an item: in the work order (korder[k] =
   // b * n_kt + kt names the k-th key tile, whose Hkv KV heads are
-  // consecutive items), else key tiles outer and rows inner.
+  // consecutive items), in the row-local order (the key tiles of one (batch,
+  // KV head) one after another on one XCD, as for the query tiles), else
+  // key tiles outer and rows inner.
   auto decode = [&](int item, int& ib, int& ikvh, int& ikt) {
     if (a.korder != nullptr) {
       const int k = item / a.Hkv;
@@ -274,6 +276,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       const int e = a.korder[k];
       ib = e / n_kt;
       ikt = e - ib * n_kt;
+    } else if (a.local_order) {
+      const int e = xcd_chunk_entry(item, n_items);
+      ikt = e % n_kt;
+      const int bk = e / n_kt;
+      ib = bk / a.Hkv;
+      ikvh = bk - ib * a.Hkv;
     } else {
       const int row = item % rows;
       ikt = item / rows;
@@ -656,6 +664,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   const int n_qt = (T + C::kBM - 1) / C::kBM;
   static_assert(C::kBM == kOrderRows && C::kBN == kOrderTile, "the work order counts this tiling");
   int b, h, qt;
+  // The row-local order is not used here: in a same-box A/B on C4's window
+  // layers it halved this kernel's HBM reads but cost 2% of its time.
   if (a.qorder != nullptr) {
     ordered_query_item(blockIdx.x, a.qorder, n_qt, a.H, a.Hkv, a.group, b, h, qt);
   } else {

@@ -162,6 +162,32 @@ __device__ inline void query_row(int r, int B, int Hkv, int group, int& b, int& 
   h = (bkv - b * Hkv) * group + gi;
 }
 
+// Position of item id in a list dealt to the XCDs in contiguous chunks: the
+// hardware sends id to XCD id % 8, in increasing id, so XCD x runs list
+// entries x*q + min(x, r) onward (q, r = n_items / 8, n_items % 8) in list
+// order.
+__device__ inline int xcd_chunk_entry(int id, int n_items) {
+  constexpr int X = 8;
+  const int x = id % X, s = id / X, q = n_items / X, r = n_items % X;
+  return x * q + min(x, r) + s;
+}
+
+// (batch, query head, query tile) of item id in the row-local order: the list
+// runs over (batch, KV head) outer, query tile (last first: the first tiles
+// of a row see fewer keys, so each XCD's part ends on light tiles), then the
+// KV head's group of query heads, and each XCD takes a contiguous part of it,
+// so the tiles of a row (and the heads that share its K and V) run together
+// on one XCD.
+__device__ inline void local_query_item(int id, int n_items, int n_tiles, int Hkv, int group, int& b, int& h,
+                                        int& tile) {
+  const int e = xcd_chunk_entry(id, n_items);
+  const int gi = e % group, t = e / group;
+  tile = n_tiles - 1 - t % n_tiles;
+  const int bk = t / n_tiles;
+  b = bk / Hkv;
+  h = (bk - b * Hkv) * group + gi;
+}
+
 // (batch, query head, query tile) of item id of a query-tile grid taken in a
 // work order: order[k] = b * n_tiles + tile names the k-th tile, whose H
 // heads are the ids k*H .. k*H + H-1, numbered like query_row's rows of one

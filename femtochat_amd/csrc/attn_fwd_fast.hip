@@ -97,6 +97,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
   int b, h, qt;
   if (a.order != nullptr) {
     ordered_query_item(blockIdx.x, a.order, n_qt, a.H, a.Hkv, a.group, b, h, qt);
+  } else if (a.local_order) {
+    local_query_item(blockIdx.x, (int)gridDim.x, n_qt, a.Hkv, a.group, b, h, qt);
   } else {
     const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);
     qt = n_qt - 1 - it0.rank;  // longest query tiles first

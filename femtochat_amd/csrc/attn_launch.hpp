@@ -17,6 +17,7 @@ struct FwdArgs {
   const void* V;
   const int32_t* pos;
   const int32_t* order;  // fast mode with positions: query tiles in work order, or null
+  int local_order;       // fast mode, narrow window: row-local order (windowed())
   void* O;
   float* l;
   float* m;
@@ -72,6 +73,7 @@ struct BwdArgs {
   const int32_t* chunk_lb;
   const int32_t* qorder;  // fast mode with positions: dQ tiles in work order, or null
   const int32_t* korder;  // and the dK/dV kernel's key tiles, or null
+  int local_order;        // fast mode, narrow window: the dK/dV kernel's key tiles in row-local order (windowed())
   void* dQ;
   void* dK;
   void* dV;

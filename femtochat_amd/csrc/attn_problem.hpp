@@ -46,6 +46,15 @@ inline bool order_fits(int T, int B) { return (int64_t)B * ((T + kOrderRows - 1)
 // kernel's tables fit.
 inline bool ordered(const Problem& p) { return p.bf16 && p.positions && order_fits(p.T, p.B); }
 
+// A sliding window at most half the sequence (no positions): the tiles of a
+// row do about the same work and consecutive tiles share most of their keys,
+// so the fast forward and dK/dV kernels take each row's tiles one after
+// another on one XCD (row-local order) instead of the longest-first order
+// over all rows, which halves their HBM reads.
+inline bool windowed(const Problem& p) {
+  return p.bf16 && !p.positions && (int64_t)p.left + std::max(p.right, 0) + 1 <= p.T / 2;
+}
+
 // Head dims the kernels are compiled for.
 inline bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 

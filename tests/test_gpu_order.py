@@ -34,6 +34,9 @@ CASES = [
     (2, 777, 2, 1, 64, (300, 0), 150),
     (1, 515, 2, 2, 32, (200, 40), 60),
     (4, 256, 2, 1, 128, (-1, 0), 500),
+    (1, 1, 2, 1, 64, (-1, 0), 5),        # one query
+    (2, 129, 2, 2, 16, (-1, 0), 10),     # one query past a tile
+    (3, 300, 4, 1, 32, (0, 0), 30),      # each query sees only itself
 ]
 
 
@@ -185,3 +188,30 @@ def test_order_repeats_and_shrinks(gpu):
         outs.append((O, l, m) + tuple(g))
     for a, b in zip(outs[0], outs[2]):
         assert torch.equal(a, b)
+
+
+def test_order_limit_gives_the_same_bits(gpu):
+    """Past the order kernel's table (B * ceil(T/128) > 4096) the kernels fall
+    back to the index order; per-row results must not depend on which: the
+    33-row problem (unordered) equals its two halves run separately (each
+    ordered), bit for bit."""
+    A = MFMAFast()
+    B, T, H, Hkv, D = 33, 16384, 1, 1, 16
+    assert B * (-(-T // 128)) > 4096 and 17 * (-(-T // 128)) <= 4096
+    positions = W.document_positions(T, B, seed=11, mean=600, sigma=1.0, cap=6000)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    Qd, Kd, Vd = (torch.randn(B, T, n, D, device=gpu, generator=g).bfloat16() for n in (H, Hkv, Hkv))
+    dOd = (0.1 * torch.randn(B, T, H, D, device=gpu, generator=g)).bfloat16()
+    pos_d = torch.from_numpy(positions).to(gpu)
+    assert Kn.forward_workspace_bytes(A, Qd, Kd, positions=pos_d) == 0
+    fwd = _forward_abi(A, Qd, Kd, Vd, (-1, 0), pos_d, None)
+    full = fwd + gpu_backward(A, dOd, Qd, Kd, Vd, *fwd, (-1, 0), pos_d)
+    for rows in (slice(0, 16), slice(16, 33)):
+        sub = [x[rows].contiguous() for x in (Qd, Kd, Vd, dOd, pos_d)]
+        ws = torch.empty(Kn.forward_workspace_bytes(A, sub[0], sub[1], positions=sub[4]) - 256, dtype=torch.uint8,
+                         device=gpu)
+        O, l, m = _forward_abi(A, sub[0], sub[1], sub[2], (-1, 0), sub[4], ws)
+        part = (O, l, m) + gpu_backward(A, sub[3], sub[0], sub[1], sub[2], O, l, m, (-1, 0), sub[4])
+        torch.cuda.synchronize()
+        for name, a, b in zip(("O", "l", "m", "dQ", "dK", "dV"), part, full):
+            assert torch.equal(a, b[rows]), f"the order changed {name}"

@@ -283,12 +283,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
       }
       const int nmf = (bS < NKB ? NQB * KC : 0) + (bP >= 0 ? NQB * 2 * DB : 0);
       const bool valu = bX >= 0 && bX < NKB;
-      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 6, 0);
 #pragma unroll
       for (int i = 0; i < 2 * NQB * (KC > 2 * DB ? KC : 2 * DB); ++i) {
         if (i < nmf) {
           __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
           if (valu) __builtin_amdgcn_sched_group_barrier(kSchedVALU, 6, 0);
         }
       }

@@ -59,13 +59,19 @@ __device__ inline float other_half(float v) {
 }
 
 // Masks the scores of a 32-key block (S^T, lane = query) outside [lb, ub]:
-// key = k0 + acc_row(r, g).
+// key = k0 + acc_row(r, g).  kLower / kUpper test only the bound that can
+// cut the tile (a tile below every row's upper bound needs no upper test).
+constexpr int kLower = 1, kUpper = 2, kBoth = kLower | kUpper;
+template <int kSides = kBoth>
 __device__ inline void mask_block(f32x16& s, int k0, int g, int lb, int ub) {
   const int x = k0 + 4 * g - lb, y = ub - (k0 + 4 * g);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int c = 8 * (r >> 2) + (r & 3);
-    s[r] = ((x >= -c) & (y >= c)) ? s[r] : -INFINITY;
+    bool in = true;
+    if (kSides & kLower) in = in & (x >= -c);
+    if (kSides & kUpper) in = in & (y >= c);
+    s[r] = in ? s[r] : -INFINITY;
   }
 }
 
@@ -235,7 +241,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
   };
 
   auto body = [&](auto mask_tag, int kt, const char* Ks) {
-    constexpr bool need_mask = decltype(mask_tag)::value;
+    constexpr int kSides = decltype(mask_tag)::value;  // bounds that cut the tile (0: none)
+    constexpr bool need_mask = kSides != 0;
     const char* Vs = Ks + C::kTileBytes;
     f32x16 s[NKB][NQB];
     bf16x8 pf[NKB][NQB][2];
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
       if (bX >= 0 && bX < NKB) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
-          if (need_mask) mask_block(s[bX][qb], kt + 32 * bX, g, lb[qb], ub[qb]);
+          if (need_mask) mask_block<kSides>(s[bX][qb], kt + 32 * bX, g, lb[qb], ub[qb]);
           const float mq = block_max(s[bX][qb], qb);
           // A row's first visible key sets the reference (nothing to rescale).
           m_ref[qb] = m_ref[qb] == -INFINITY ? mq : m_ref[qb];
@@ -302,8 +309,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
       for (int k = 0; k < NDMA; ++k) dma_part(k);
       return;
     }
-    if (wlb_max <= kt && kt + BN - 1 <= wub_min) body(std::false_type{}, kt, Ks);
-    else body(std::true_type{}, kt, Ks);
+    const bool lower = wlb_max > kt, upper = kt + BN - 1 > wub_min;
+    if (!lower && !upper) body(std::integral_constant<int, 0>{}, kt, Ks);
+    else if (!lower) body(std::integral_constant<int, kUpper>{}, kt, Ks);
+    else if (!upper) body(std::integral_constant<int, kLower>{}, kt, Ks);
+    else body(std::integral_constant<int, kBoth>{}, kt, Ks);
   };
 
   if (ntiles > 0) {

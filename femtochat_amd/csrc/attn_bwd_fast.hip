@@ -57,7 +57,7 @@ struct DkdvStep {
   // calls it at its phase boundaries so the loads queue behind the products
   // instead of all at once.
   template <typename Dma>
-  __device__ static inline void run(const Dma& dma, const char* Qs, const char* Os, const float* lse,
+  __device__ __attribute__((always_inline)) static inline void run(const Dma& dma, const char* Qs, const char* Os, const float* lse,
                                     const float* delta, const int* lbs, const int* lbc, const bf16x8* kf,
                                     const bf16x8* vf, f32x16* dk, f32x16* dv, const FragOffsets<D>& fo, int q0,
                                     int key, int kw0, int kw1, int g, int T, int right, float c2) {
@@ -79,11 +79,17 @@ struct DkdvStep {
       for (int k = 0; k < NPH; ++k) dma(k);
       return;
     }
-    // Two straight-line bodies: tiles inside every window skip the mask.
-    if (lbmax <= kw0 && kw1 <= ubmin)
-      body<false>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+    // Straight-line bodies: steps inside every row's window skip the mask,
+    // steps cut by only one side of it test only that side.
+    const bool lower = lbmax > kw0, upper = kw1 > ubmin;
+    if (!lower && !upper)
+      body<0>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+    else if (!lower)
+      body<kUpper>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+    else if (!upper)
+      body<kLower>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
     else
-      body<true>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
+      body<kBoth>(dma, Qs, Os, lse, delta, lbs, kf, vf, dk, dv, fo, q0, key, g, T, right, c2);
   }
 
   __device__ static inline void stats(const float* lse, const float* delta, int qb, int g, f32x4* L, f32x4* Dl) {
@@ -107,12 +113,13 @@ struct DkdvStep {
 
   // P = exp2(S c2 - lse2), dS = P (dP - Delta), both rounded to bf16 as the
   // operands of dV += P^T dO and dK += dS^T Q.
-  // The mask (need_mask) is branch-free: P is zero unless key >= lb(q) and
-  // key - q <= right, dS = P (dP - Delta) z(q) with z = 0 on rows with a single
-  // visible key.  Rows at or beyond T have lse2 = +inf, so P and dS vanish
-  // there without a test.
-  template <bool need_mask>
-  __device__ static inline void softmax(f32x16& s, f32x16& dp, const f32x4* L, const f32x4* Dl, const i32x4* LB,
+  // The mask (kSides != 0) is branch-free: P is zero unless key >= lb(q)
+  // (kLower) and key - q <= right (kUpper), dS = P (dP - Delta) z(q) with
+  // z = 0 on rows with a single visible key.  Rows at or beyond T have
+  // lse2 = +inf, so P and dS vanish there without a test; a key at or past T
+  // only occurs in steps that test the upper side.
+  template <int kSides>
+  __device__ __attribute__((always_inline)) static inline void softmax(f32x16& s, f32x16& dp, const f32x4* L, const f32x4* Dl, const i32x4* LB,
                                         const f32x4* Z, int qb, int q0, int key, int g, int T, int right, float c2,
                                         bf16x8* pf, bf16x8* sf) {
     // key - q <= right  <=>  x >= -(8j + t) for row 4g + 8j + t; a key at or
@@ -125,12 +132,10 @@ struct DkdvStep {
       for (int t = 0; t < 4; ++t) {
         const int r = 4 * j + t;
         float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -L[j][t]));
-        if (need_mask) {
-          p = x >= -(8 * j + t) ? p : 0.0f;
-          p = key >= LB[j][t] ? p : 0.0f;
-        }
+        if (kSides & kUpper) p = x >= -(8 * j + t) ? p : 0.0f;
+        if (kSides & kLower) p = key >= LB[j][t] ? p : 0.0f;
         float ds = p * (dp[r] - Dl[j][t]);
-        if (need_mask) ds *= Z[j][t];
+        if (kSides) ds *= Z[j][t];
         s[r] = p;
         dp[r] = ds;
       }
@@ -146,8 +151,8 @@ struct DkdvStep {
     return lds_tr_frag(tile + (32 * qb + 16 * h) * 2 * D, fo.tr(0, db), fo.tr(1, db));
   }
 
-  template <bool need_mask, typename Dma>
-  __device__ static inline void body(const Dma& dma, const char* Qs, const char* Os, const float* lse,
+  template <int kSides, typename Dma>
+  __device__ __attribute__((always_inline)) static inline void body(const Dma& dma, const char* Qs, const char* Os, const float* lse,
                                      const float* delta, const int* lbs, const bf16x8* kf, const bf16x8* vf,
                                      f32x16* dk, f32x16* dv, const FragOffsets<D>& fo, int q0, int key, int g,
                                      int T, int right, float c2) {
@@ -174,7 +179,7 @@ struct DkdvStep {
           oa[c] = as_bf16x8(lds_load16(ot, fo.nat(c)));
         }
         stats(lse, delta, b1, g, L[b1], Dl[b1]);
-        if (need_mask) bounds(lbs, b1, g, LB[b1], Z[b1]);
+        if (kSides) bounds(lbs, b1, g, LB[b1], Z[b1]);
         s[b1] = zero16();
         dp[b1] = zero16();
 #pragma unroll
@@ -197,7 +202,7 @@ struct DkdvStep {
         }
       }
       if (bs >= 0 && bs < NQB) {
-        softmax<need_mask>(s[bs], dp[bs], L[bs], Dl[bs], LB[bs], Z[bs], bs, q0, key, g, T, right, c2, pf[bs],
+        softmax<kSides>(s[bs], dp[bs], L[bs], Dl[bs], LB[bs], Z[bs], bs, q0, key, g, T, right, c2, pf[bs],
                            sf[bs]);
         // First transposed fragments of the block, for the next phase.
 #pragma unroll
@@ -451,7 +456,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       s_lbc[slot][1][tid] = hi;
     }
   };
-  auto compute = [&](Step st, const char* buf, int slot) {
+  // Inlined by force: with four step bodies per buffer the compiler would
+  // otherwise make this a call (all live registers saved around it).
+  auto compute = [&](Step st, const char* buf, int slot) __attribute__((always_inline)) {
     const int q0 = (qt_begin + st.t) * BQ;
     DkdvStep<D>::run(dma_part, buf, buf + C::kTileBytes, s_lse[slot], s_delta[slot], s_lb[slot], s_lbc[slot][0], kf, vf, dk, dv,
                      fo, q0, key, kw0, kw1, g, T, a.right, c2);

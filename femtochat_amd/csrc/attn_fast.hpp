@@ -59,6 +59,12 @@ struct SwzTile {
   __device__ static constexpr int offset(int r, int u) { return r * kRowBytes + 16 * (u ^ swz(r)); }
 };
 
+// Which key bounds a masked tile body tests: kLower (key >= the row's lower
+// bound), kUpper (key <= its upper bound) or both; a tile that no row's
+// upper bound cuts (all its keys at or below every row's ub) needs no upper
+// test, and likewise for the lower bound.
+constexpr int kLower = 1, kUpper = 2, kBoth = kLower | kUpper;
+
 // 16 bytes at a byte offset of an LDS buffer.
 __device__ inline uint4 lds_load16(const char* lds, int off) { return *reinterpret_cast<const uint4*>(lds + off); }
 __device__ inline void lds_store16(char* lds, int off, uint4 v) { *reinterpret_cast<uint4*>(lds + off) = v; }

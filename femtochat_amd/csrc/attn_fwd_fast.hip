@@ -59,9 +59,7 @@ __device__ inline float other_half(float v) {
 }
 
 // Masks the scores of a 32-key block (S^T, lane = query) outside [lb, ub]:
-// key = k0 + acc_row(r, g).  kLower / kUpper test only the bound that can
-// cut the tile (a tile below every row's upper bound needs no upper test).
-constexpr int kLower = 1, kUpper = 2, kBoth = kLower | kUpper;
+// key = k0 + acc_row(r, g), testing only the bounds in kSides.
 template <int kSides = kBoth>
 __device__ inline void mask_block(f32x16& s, int k0, int g, int lb, int ub) {
   const int x = k0 + 4 * g - lb, y = ub - (k0 + 4 * g);

@@ -805,18 +805,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
       dma_part(ph);
       __builtin_amdgcn_sched_barrier(0);
       if (b1 < NKB) {
-        bf16x8 ka[KC], va[KC];
-#pragma unroll
-        for (int c = 0; c < KC; ++c) {
-          ka[c] = as_bf16x8(lds_load16(Ks + 32 * b1 * 2 * D, fo.nat(c)));
-          va[c] = as_bf16x8(lds_load16(Vs + 32 * b1 * 2 * D, fo.nat(c)));
-        }
         s[b1] = zero16();
         dp[b1] = zero16();
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
-          s[b1] = M::mma(ka[c], qf[c], s[b1]);
-          dp[b1] = M::mma(va[c], of[c], dp[b1]);
+          const bf16x8 ka = as_bf16x8(lds_load16(Ks + 32 * b1 * 2 * D, fo.nat(c)));
+          s[b1] = M::mma(ka, qf[c], s[b1]);
+        }
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          const bf16x8 va = as_bf16x8(lds_load16(Vs + 32 * b1 * 2 * D, fo.nat(c)));
+          dp[b1] = M::mma(va, of[c], dp[b1]);
         }
       }
       if (b2 >= 0) {

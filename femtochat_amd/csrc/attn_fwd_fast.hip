@@ -380,28 +380,64 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
     }
   }
 
+  // O goes out through LDS (the stage buffers are idle after the tile loop's
+  // last barrier): each wave writes its 32 rows x D into a row-major tile of
+  // its own, 16-byte units XOR-swizzled by the row, then stores whole rows
+  // at 16 bytes per lane (a store instruction covers 64 / U full rows)
+  // instead of 16 bytes of each of 32 rows.
+  static_assert(NQB == 1, "one 32-query block per wave");
+  auto store_o = [&](auto elem) __attribute__((always_inline)) {
+    using E = decltype(elem);
+    constexpr int RB = D * (int)sizeof(E);  // bytes per output row
+    constexpr int U = RB / 16;              // 16-byte units per row
+    static_assert(2 * 32 * RB <= C::kStageBytes, "two waves' tiles per stage buffer");
+    char* tile = (wave < 2 ? bufA : bufB) + (wave & 1) * (32 * RB);
+    const float lt = l_half[0] + other_half(l_half[0]);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 32 * db + 8 * j + 4 * g;  // four consecutive d of row l32
+        if (d0 < D) {
+          const int byte = d0 * (int)sizeof(E);
+          const int at = l32 * RB + 16 * ((byte / 16) ^ (l32 & (U - 1))) + byte % 16;
+          float v[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = o[0][db][4 * j + t] * inv;
+          if constexpr (sizeof(E) == 2) {
+            auto pack = [](float x, float y) __attribute__((always_inline)) {
+              return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
+                     ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
+            };
+            *reinterpret_cast<uint2*>(tile + at) = make_uint2(pack(v[0], v[1]), pack(v[2], v[3]));
+          } else {
+            *reinterpret_cast<uint4*>(tile + at) =
+                make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+          }
+        }
+      }
+    }
+    constexpr int RPI = 64 / U;  // rows per store instruction
+    const int q0w = qv[0] - l32;  // the wave's first query
+    char* obase = static_cast<char*>(a.O) + (((int64_t)b * T * a.H + h) * D) * (int64_t)sizeof(E);
+    const int64_t opitch = (int64_t)a.H * RB;  // bytes between consecutive queries
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int row = i * RPI + lane / U, u = lane % U;
+      const uint4 val = *reinterpret_cast<const uint4*>(tile + row * RB + 16 * (u ^ (row & (U - 1))));
+      if (q0w + row < T) *reinterpret_cast<uint4*>(obase + (q0w + row) * opitch + 16 * u) = val;
+    }
+  };
+  if (a.out_bf16) store_o(bf16{});
+  else store_o(0.0f);
+
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     const int q = qv[qb];
     const float mt = m_true[qb];
     const float lt = l_half[qb] + other_half(l_half[qb]);
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (q < T) {
-      const int64_t orow = ((int64_t)b * T + q) * a.H + h;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d0 = 32 * db + 8 * j + 4 * g;
-          if (d0 < D) {
-            f32x4 v;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v[t] = o[qb][db][4 * j + t] * inv;
-            if (a.out_bf16) store4(static_cast<bf16*>(a.O) + orow * D + d0, v, false);
-            else store4(static_cast<float*>(a.O) + orow * D + d0, v, false);
-          }
-        }
-      }
       if (g == 0) {
         const int64_t si = ((int64_t)b * a.H + h) * T + q;
         const bool any = mt != -INFINITY;

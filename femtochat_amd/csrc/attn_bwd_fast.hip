@@ -885,22 +885,66 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
     dma_wait_barrier();
   }
 
-  if (q < T) {
-    const int64_t orow = ((int64_t)b * T + q) * a.H + h;
+  // dQ goes out through LDS (the stage buffers are idle after the tile loop's
+  // last barrier): each wave writes its 32 rows x D of scaled fp32 dQ into a
+  // row-major tile of its own, 16-byte units XOR-swizzled by the row, then
+  // takes whole rows, 16 bytes of output per lane (plus the caller's values
+  // when accumulating, added in fp32 before the one rounding).
+  {
+    constexpr int RB = 4 * D;  // bytes per staged fp32 row
+    constexpr int U = RB / 16;
+    static_assert(2 * 32 * RB <= C::kStageBytes, "two waves' tiles per stage buffer");
+    char* tile = (wave < 2 ? bufA : bufB) + (wave & 1) * (32 * RB);
+    auto unit_at = [&](int row, int u) { return row * RB + 16 * (u ^ (row & (U - 1))); };
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int d0 = 32 * db + 8 * j + 4 * g;
+        const int d0 = 32 * db + 8 * j + 4 * g;  // four consecutive d of row l32
         if (d0 < D) {
-          f32x4 v;
+          float v[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) v[t] = dq[db][4 * j + t] * a.scale;
-          if (a.grad_bf16) store4(static_cast<bf16*>(a.dQ) + orow * D + d0, v, a.accumulate);
-          else store4(static_cast<float*>(a.dQ) + orow * D + d0, v, a.accumulate);
+          *reinterpret_cast<uint4*>(tile + unit_at(l32, d0 / 4)) =
+              make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
         }
       }
     }
+    const int q0w = q - l32;  // the wave's first query
+    auto emit = [&](auto elem) __attribute__((always_inline)) {
+      using E = decltype(elem);
+      constexpr int EPL = 16 / (int)sizeof(E);  // output elements per lane
+      constexpr int LPR = D / EPL;              // lanes per row
+      constexpr int RPI = 64 / LPR;             // rows per instruction
+      E* base = static_cast<E*>(a.dQ) + ((int64_t)b * T * a.H + h) * D;
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int row = i * RPI + lane / LPR, e0 = EPL * (lane % LPR);
+        float v[EPL];
+#pragma unroll
+        for (int k = 0; k < EPL / 4; ++k) {
+          const uint4 w = *reinterpret_cast<const uint4*>(tile + unit_at(row, e0 / 4 + k));
+          v[4 * k] = __uint_as_float(w.x), v[4 * k + 1] = __uint_as_float(w.y);
+          v[4 * k + 2] = __uint_as_float(w.z), v[4 * k + 3] = __uint_as_float(w.w);
+        }
+        if (q0w + row < T) {
+          E* p = base + (int64_t)(q0w + row) * a.H * D + e0;
+          if (a.accumulate) {
+            const uint4 old = *reinterpret_cast<const uint4*>(p);
+            const E* o = reinterpret_cast<const E*>(&old);
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) v[k] += to_f32(o[k]);
+          }
+          uint4 out;
+          E* po = reinterpret_cast<E*>(&out);
+#pragma unroll
+          for (int k = 0; k < EPL; ++k) po[k] = from_f32<E>(v[k]);
+          *reinterpret_cast<uint4*>(p) = out;
+        }
+      }
+    };
+    if (a.grad_bf16) emit(bf16{});
+    else emit(0.0f);
   }
 }
 

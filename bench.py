@@ -441,7 +441,7 @@ def main() -> int:
     # parity cases in tests/, timed here beside the headline.
     configs = {}
     for name in [c for c in args.configs.split(",") if c and c != wl.name]:
-        r = measure_attention(W.WORKLOADS[name], dev, max(3, args.steps // 2), max(2, args.warmup // 2))
+        r = measure_attention(W.WORKLOADS[name], dev, max(3, args.steps), max(2, args.warmup))
         r.pop("raw")
         configs[name] = r
 

@@ -215,3 +215,29 @@ def test_order_limit_gives_the_same_bits(gpu):
         torch.cuda.synchronize()
         for name, a, b in zip(("O", "l", "m", "dQ", "dK", "dV"), part, full):
             assert torch.equal(a, b[rows]), f"the order changed {name}"
+
+
+@pytest.mark.parametrize("window,T", [((100, 0), 700), ((300, 20), 1024)])
+def test_row_local_order_gives_the_same_bits(gpu, window, T):
+    """A window of at most half the sequence takes the row-local order (forward
+    and dK/dV); positions that restart nowhere (positions[q] = q) leave the mask
+    unchanged but take the work order instead.  Same mask, same bits."""
+    A = MFMAFast()
+    B, H, Hkv, D = 3, 4, 2, 64
+    assert window[0] + max(window[1], 0) + 1 <= T // 2  # the row-local order applies
+    Q, K, V, dO = _inputs(T + 7, B, T, H, Hkv, D)
+    Qd, Kd, Vd, dOd = (torch.from_numpy(x).to(gpu, torch.bfloat16).contiguous() for x in (Q, K, V, dO))
+    linear = torch.arange(T, dtype=torch.int32, device=gpu).repeat(B, 1).contiguous()
+    outs = []
+    for pos in (None, linear):
+        ws = None
+        n = Kn.forward_workspace_bytes(A, Qd, Kd, positions=pos)
+        if n:
+            ws = torch.empty(n - 256, dtype=torch.uint8, device=gpu)
+        fwd = _forward_abi(A, Qd, Kd, Vd, window, pos, ws)
+        outs.append(fwd + gpu_backward(A, dOd, Qd, Kd, Vd, *fwd, window, pos))
+    torch.cuda.synchronize()
+    for name, a, b in zip(("O", "l", "m", "dQ", "dK", "dV"), *outs):
+        assert torch.equal(a, b), f"{name} differs between the row-local and the work order"
+    O_ref, l_ref, m_ref = R.forward(Q, K, V, window, None)
+    assert rel_err(to_np(outs[0][0]), O_ref) <= TOL["fast"]

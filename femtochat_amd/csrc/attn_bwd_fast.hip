@@ -5,17 +5,19 @@
 // rounded to bf16 before their second product and dS = 0 for a query with a
 // single visible key, ext/FemtoChatCUDAExt.jl:1915-1946).
 //
-//  * attn_bwd_dkdv_fast: a workgroup owns 128 keys of one (batch, KV head);
-//    each wave keeps its 32 keys' K and V in registers (B operands of
-//    S = Q K^T and dP = dO V^T), loops over the GQA group's heads and the query
-//    tiles (128 queries) that can see the keys, and accumulates dK and dV in
-//    registers.  Q and dO tiles are staged once into swizzled LDS and read both
-//    as natural fragments (for S, dP) and through ds_read_b64_tr_b16 (for
-//    dV += P^T dO and dK += dS^T Q).
+//  * attn_bwd_dkdv_fast: persistent, one workgroup per CU; an item is 128
+//    keys of one (batch, KV head), taken heaviest first from a counter per
+//    XCD (or in the work order with positions, or row by row for a narrow
+//    window).  Each wave keeps its 32 keys' K and V in registers (B operands
+//    of S = Q K^T and dP = dO V^T), loops over the GQA group's heads and the
+//    query tiles (128 queries) that can see the keys, and accumulates dK and
+//    dV in registers.  Q and dO tiles are staged once into swizzled LDS and
+//    read both as natural fragments (for S, dP) and through
+//    ds_read_b64_tr_b16 (for dV += P^T dO and dK += dS^T Q).
 //  * attn_bwd_dq_fast: a workgroup owns 128 queries of one (batch, head);
 //    S^T and dP^T are recomputed with the query as the lane index so dS^T is
 //    directly the B operand of dQ^T += K^T dS^T; K and V tiles are staged once
-//    and K is also read transposed.
+//    and K is also read transposed; dQ leaves through LDS in whole rows.
 #include "attn_fast.hpp"
 #include "attn_launch.hpp"
 

@@ -29,7 +29,8 @@
 // block maximum beyond that flags the wave, which then recomputes its rows
 // after the tile loop with a plain two-pass method (exact maximum first)
 // reading K and V from global memory.  P is rounded to bf16 against m_ref and
-// the row sum is taken over unrounded P, as in the reference.
+// the row sum is taken over unrounded P, as in the reference.  O leaves
+// through LDS in whole rows.
 #include "attn_fast.hpp"
 #include "attn_launch.hpp"
 

@@ -326,12 +326,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   // With positions, a query tile is skipped when no query of it can see a key
   // of [k0, k1] (its smallest key lower bound exceeds k1).  The answers are
   // tabulated in LDS per item so the step loop reads no global memory.
+  // The chunk index is clamped rather than tested, so the loads issue
+  // together (one memory round trip, not one per chunk): a clamped index
+  // repeats the tile's last chunk, which leaves the minimum unchanged.
   auto tile_visible_global = [&](int qt) -> bool {
     const int c0 = (qt * BQ) / 32;
     int lo = clb[2 * c0];
 #pragma unroll
-    for (int c = 1; c < BQ / 32; ++c)
-      if (c0 + c < nchunks) lo = min(lo, clb[2 * (c0 + c)]);
+    for (int c = 1; c < BQ / 32; ++c) lo = min(lo, clb[2 * min(c0 + c, nchunks - 1)]);
     return lo <= k1;
   };
   auto tile_visible = [&](int qt) -> bool {
@@ -705,8 +707,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
     s_bounds[1][wave] = wub_max;
   }
   const int64_t si = ((int64_t)b * a.H + h) * T + q;
+  // The row's statistics (l and m, or lse2 and Delta) load first and
+  // unconditionally (a query past T reads row T-1 and discards it), so they
+  // share one memory round trip with the fragment loads below.
+  const int64_t sc = si - q + min(q, T - 1);
+  const float st_a = (a.stats ? a.m : a.lse2)[sc];
+  const float st_b = (a.stats ? a.l : a.delta)[sc];
 
-  bf16x8 qf[KC], of[KC];
+  bf16x8 qf[KC], of[KC], ov[KC];
   const int qoff = q * qpitch + 16 * g;
   {
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(static_cast<const char*>(a.Q) + hoff, (uint32_t)qrec);
@@ -716,41 +724,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
       qf[c] = as_bf16x8(buf_load16(rq, qoff + 32 * c, 0));
       of[c] = as_bf16x8(buf_load16(ro, qoff + 32 * c, 0));
     }
-  }
-  float neg_lse, dlt;
-  if (a.stats) {
-    // The backward preprocess for this workgroup's queries (the sum over D
-    // is split between the two half-waves, which hold alternate 8-element
-    // runs of the head dimension), written out for the dK/dV kernel.
-    const __amdgpu_buffer_rsrc_t rO = make_rsrc(static_cast<const char*>(a.O) + hoff, (uint32_t)qrec);
-    float part = 0.0f;
+    if (a.stats) {
+      const __amdgpu_buffer_rsrc_t rO = make_rsrc(static_cast<const char*>(a.O) + hoff, (uint32_t)qrec);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const bf16x8 ov = as_bf16x8(buf_load16(rO, qoff + 32 * c, 0));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part += static_cast<float>(of[c][e]) * static_cast<float>(ov[e]);
+      for (int c = 0; c < KC; ++c) ov[c] = as_bf16x8(buf_load16(rO, qoff + 32 * c, 0));
     }
-    dlt = part + __shfl_xor(part, 32);
-    float lse2 = INFINITY;
-    if (q < T) lse2 = a.m[si] * kLog2e + __builtin_amdgcn_logf(fmaxf(a.l[si], kFltEps));
-    if (q < T && g == 0) {
-      a.delta_out[si] = dlt;
-      a.lse2_out[si] = lse2;
-    }
-    neg_lse = -lse2;
-    dlt = q < T ? dlt : 0.0f;
-  } else {
-    neg_lse = q < T ? -a.lse2[si] : -INFINITY;
-    dlt = q < T ? a.delta[si] : 0.0f;
   }
   FragOffsets<D> fo;
   fo.init(lane);
   DmaPlan<D, BN> plan;
   plan.init(wave, lane, kpitch);
-  f32x16 dq[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i) dq[i] = zero16();
-  const float c2 = a.scale_log2;
 
   __syncthreads();
   int kmin = s_bounds[0][0], kmax = s_bounds[1][0];
@@ -790,6 +773,35 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
       nx_v = buffer_words(Vb, 0);
     }
   };
+  // The first tile's loads go out before anything waits for the loads above.
+  if (ntiles > 0) {
+    issue(0, bufA);
+#pragma unroll
+    for (int k = 0; k < NPH; ++k) dma_part(k);
+  }
+
+  float neg_lse, dlt;
+  if (a.stats) {
+    // The backward preprocess for this workgroup's queries (the sum over D
+    // is split between the two half-waves, which hold alternate 8-element
+    // runs of the head dimension), written out for the dK/dV kernel.
+    float part = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += static_cast<float>(of[c][e]) * static_cast<float>(ov[c][e]);
+    }
+    dlt = part + __shfl_xor(part, 32);
+    neg_lse = q < T ? -(st_a * kLog2e + __builtin_amdgcn_logf(fmaxf(st_b, kFltEps))) : -INFINITY;
+    dlt = q < T ? dlt : 0.0f;
+  } else {
+    neg_lse = q < T ? -st_a : -INFINITY;
+    dlt = q < T ? st_b : 0.0f;
+  }
+  f32x16 dq[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) dq[i] = zero16();
+  const float c2 = a.scale_log2;
 
   // Tile body: a pipeline over the tile's two 32-key blocks, phase i holding
   // S^T, dP^T of block i, the softmax of block i-1 and dQ^T += K^T dS^T of
@@ -871,11 +883,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
     else body(std::true_type{}, kt, Ks);
   };
 
-  if (ntiles > 0) {
-    issue(0, bufA);
-#pragma unroll
-    for (int k = 0; k < NPH; ++k) dma_part(k);
-  }
   dma_wait_barrier();
   for (int it = 0; it < ntiles; it += 2) {
     issue(it + 1, bufB);
@@ -885,6 +892,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
     issue(it + 2, bufA);
     compute(it + 1, bufB);
     dma_wait_barrier();
+  }
+
+  // Delta and lse2 for the dK/dV kernel, stored after the tile loop so that
+  // its first barrier does not wait for them.
+  if (a.stats && q < T && g == 0) {
+    a.delta_out[si] = dlt;
+    a.lse2_out[si] = -neg_lse;
   }
 
   // dQ goes out through LDS (the stage buffers are idle after the tile loop's

@@ -675,8 +675,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
   const int n_qt = (T + C::kBM - 1) / C::kBM;
   static_assert(C::kBM == kOrderRows && C::kBN == kOrderTile, "the work order counts this tiling");
   int b, h, qt;
-  // The row-local order is not used here: in a same-box A/B on C4's window
-  // layers it halved this kernel's HBM reads but cost 2% of its time.
+  // The row-local order is not used here: in same-box A/B runs on C4's
+  // window layers it halved this kernel's HBM reads but cost it 1.5-2% of its
+  // time (with and without full tiles first).
   if (a.qorder != nullptr) {
     ordered_query_item(blockIdx.x, a.qorder, n_qt, a.H, a.Hkv, a.group, b, h, qt);
   } else {

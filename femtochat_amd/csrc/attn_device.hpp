@@ -172,18 +172,46 @@ __device__ inline int xcd_chunk_entry(int id, int n_items) {
   return x * q + min(x, r) + s;
 }
 
-// (batch, query head, query tile) of item id in the row-local order: the list
-// runs over (batch, KV head) outer, query tile (last first: the first tiles
-// of a row see fewer keys, so each XCD's part ends on light tiles), then the
-// KV head's group of query heads, and each XCD takes a contiguous part of it,
-// so the tiles of a row (and the heads that share its K and V) run together
-// on one XCD.
-__device__ inline void local_query_item(int id, int n_items, int n_tiles, int Hkv, int group, int& b, int& h,
-                                        int& tile) {
-  const int e = xcd_chunk_entry(id, n_items);
-  const int gi = e % group, t = e / group;
-  tile = n_tiles - 1 - t % n_tiles;
-  const int bk = t / n_tiles;
+// (batch, query head, query tile) of item id in the row-local order, for a
+// grid of B*Hkv*group*n_tiles items.  When the B*Hkv (batch, KV head) rows
+// divide into 8, each XCD takes B*Hkv/8 whole rows: first their full query
+// tiles (tile >= full_from, whose windows the sequence start does not cut),
+// row after row, tiles last first, the KV head's group of query heads
+// innermost; then their partial tiles, largest tile first, row after row.
+// The full tiles all cost the same, so an XCD's workgroups end together and
+// the hardware, which starts workgroups in order, finds a free slot for the
+// next one at once (mixing partial tiles in left slots empty for
+// microseconds); the tiles of a row, and the heads that share its K and V,
+// run together on one XCD, whose L2 then serves them.  Otherwise the list runs
+// over rows, tiles last first, then heads, in a contiguous part per XCD.
+__device__ inline void local_query_item(int id, int n_items, int n_tiles, int full_from, int B, int Hkv, int group,
+                                        int& b, int& h, int& tile) {
+  constexpr int X = 8;
+  const int rows = B * Hkv;
+  int bk, gi;
+  if (rows % X == 0) {
+    const int x = id % X, s = id / X, rx = rows / X;
+    const int per_row = (n_tiles - full_from) * group;  // full items of a row
+    const int full = rx * per_row;
+    if (s < full) {
+      const int r = s / per_row, rem = s - r * per_row;
+      tile = n_tiles - 1 - rem / group;
+      gi = rem % group;
+      bk = x * rx + r;
+    } else {
+      const int s2 = s - full, per_tile = rx * group;  // partial items of one tile index
+      const int k = s2 / per_tile, rem = s2 - k * per_tile;
+      tile = full_from - 1 - k;
+      bk = x * rx + rem / group;
+      gi = rem % group;
+    }
+  } else {
+    const int e = xcd_chunk_entry(id, n_items);
+    gi = e % group;
+    const int t = e / group;
+    tile = n_tiles - 1 - t % n_tiles;
+    bk = t / n_tiles;
+  }
   b = bk / Hkv;
   h = (bk - b * Hkv) * group + gi;
 }

@@ -217,13 +217,14 @@ def test_order_limit_gives_the_same_bits(gpu):
             assert torch.equal(a, b[rows]), f"the order changed {name}"
 
 
-@pytest.mark.parametrize("window,T", [((100, 0), 700), ((300, 20), 1024)])
-def test_row_local_order_gives_the_same_bits(gpu, window, T):
-    """A window of at most half the sequence takes the row-local order (forward
-    and dK/dV); positions that restart nowhere (positions[q] = q) leave the mask
-    unchanged but take the work order instead.  Same mask, same bits."""
+@pytest.mark.parametrize("window,T,B", [((100, 0), 700, 3), ((300, 20), 1024, 3), ((200, 0), 1024, 4), ((0, 3), 640, 8)])
+def test_row_local_order_gives_the_same_bits(gpu, window, T, B):
+    """A window of at most half the sequence takes the row-local order (the
+    forward, with B*Hkv divisible by 8 its full query tiles first and then the
+    partial ones, and dK/dV); positions that restart nowhere (positions[q] = q) leave the
+    mask unchanged but take the work order instead.  Same mask, same bits."""
     A = MFMAFast()
-    B, H, Hkv, D = 3, 4, 2, 64
+    H, Hkv, D = 4, 2, 64
     assert window[0] + max(window[1], 0) + 1 <= T // 2  # the row-local order applies
     Q, K, V, dO = _inputs(T + 7, B, T, H, Hkv, D)
     Qd, Kd, Vd, dOd = (torch.from_numpy(x).to(gpu, torch.bfloat16).contiguous() for x in (Q, K, V, dO))

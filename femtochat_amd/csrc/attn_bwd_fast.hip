@@ -559,53 +559,101 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
         else v[i + 2] = recv;
       }
     };
+    if (a.grad_bf16 && !a.accumulate) {
+      // Overwritten bf16 gradients leave through LDS in whole rows: each
+      // wave writes its 32 keys' dK and dV (2 bytes per value, straight from
+      // the accumulators) into a row-major tile of its own in the idle stage
+      // buffer, 16-byte units XOR-swizzled by the row, then stores 16 bytes
+      // per lane, a store instruction covering 64 / U whole rows.  The next
+      // item's first tile loads into the other buffer, and this one is next
+      // written after the next item's first barrier.
+      constexpr int RB = 2 * D, U = RB / 16, RPI = 64 / U;
+      static_assert(kWaves * 2 * 32 * RB <= C::kStageBytes, "dK and dV tiles of every wave fit a stage buffer");
+      // An opaque zero in the tile address keeps its offsets from being
+      // hoisted out of the item loop (where they would only take registers).
+      int z;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+      char* tile = bufB + wave * (2 * 32 * RB);  // dK rows, then dV rows
+      auto at = [&](int row, int d) { return row * RB + 16 * ((d / 8) ^ (row & (U - 1))) + 2 * (d % 8); };
+      auto pack = [](float x, float y) __attribute__((always_inline)) {
+        return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
+               ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
+      };
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const int d0 = 32 * db + (l32 & ~3);
+      for (int db = 0; db < DB; ++db) {
+        const int d = 32 * db + l32 + z;
+        if (d < D) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float vk[4], vv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          vk[i] = dk[db][4 * j + i] * a.scale;
-          vv[i] = dv[db][4 * j + i];
+          for (int r = 0; r < 16; r += 2) {
+            const int row = acc_row(r, g) + z;  // rows r and r + 1 are keys row and row + 1
+            const uint32_t pk = pack(dk[db][r] * a.scale, dk[db][r + 1] * a.scale);
+            const uint32_t pv = pack(dv[db][r], dv[db][r + 1]);
+            *reinterpret_cast<unsigned short*>(tile + at(row, d)) = (unsigned short)pk;
+            *reinterpret_cast<unsigned short*>(tile + at(row + 1, d)) = (unsigned short)(pk >> 16);
+            *reinterpret_cast<unsigned short*>(tile + 32 * RB + at(row, d)) = (unsigned short)pv;
+            *reinterpret_cast<unsigned short*>(tile + 32 * RB + at(row + 1, d)) = (unsigned short)(pv >> 16);
+          }
         }
-        xpose(vk);  // all lanes take part in the exchange
-        xpose(vv);
-        if (d0 >= D) continue;  // whole quads (D is a multiple of 16)
-        const int kk = ekw0 + acc_row(4 * j, g) + q;
-        const int voff = (int)(((int64_t)kk * row_elems + d0) * esz);
-        if (a.grad_bf16) {
-          auto pack = [](float x, float y) __attribute__((always_inline)) {
-            return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
-                   ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
-          };
-          auto unpack = [](uint32_t w, float* o) __attribute__((always_inline)) {
-            o[0] = __uint_as_float(w << 16);
-            o[1] = __uint_as_float(w & 0xffff0000u);
-          };
-          if (a.accumulate) {  // out-of-range loads read zero
-            const u32x2 ok = __builtin_amdgcn_raw_buffer_load_b64(rk, voff, 0, 0);
-            const u32x2 ov = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, 0, 0);
-            float t[4];
-            unpack(ok[0], t), unpack(ok[1], t + 2);
-            for (int i = 0; i < 4; ++i) vk[i] += t[i];
-            unpack(ov[0], t), unpack(ov[1], t + 2);
-            for (int i = 0; i < 4; ++i) vv[i] += t[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int row = i * RPI + (lane + z) / U, u = (lane + z) % U;
+        const int off = row * RB + 16 * (u ^ (row & (U - 1)));
+        const uint4 k4 = *reinterpret_cast<const uint4*>(tile + off);
+        const uint4 v4 = *reinterpret_cast<const uint4*>(tile + 32 * RB + off);
+        const int voff = (int)(((int64_t)(ekw0 + row) * row_elems + 8 * u) * 2);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{k4.x, k4.y, k4.z, k4.w}, rk, voff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v4.x, v4.y, v4.z, v4.w}, rv, voff, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int d0 = 32 * db + (l32 & ~3);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float vk[4], vv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vk[i] = dk[db][4 * j + i] * a.scale;
+            vv[i] = dv[db][4 * j + i];
           }
-          __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vk[0], vk[1]), pack(vk[2], vk[3])}, rk, voff, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vv[0], vv[1]), pack(vv[2], vv[3])}, rv, voff, 0, 0);
-        } else {
-          if (a.accumulate) {
-            const u32x4 ok = __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0);
-            const u32x4 ov = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0);
-            for (int i = 0; i < 4; ++i) {
-              vk[i] += __uint_as_float(ok[i]);
-              vv[i] += __uint_as_float(ov[i]);
+          xpose(vk);  // all lanes take part in the exchange
+          xpose(vv);
+          if (d0 >= D) continue;  // whole quads (D is a multiple of 16)
+          const int kk = ekw0 + acc_row(4 * j, g) + q;
+          const int voff = (int)(((int64_t)kk * row_elems + d0) * esz);
+          if (a.grad_bf16) {
+            auto pack = [](float x, float y) __attribute__((always_inline)) {
+              return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
+                     ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
+            };
+            auto unpack = [](uint32_t w, float* o) __attribute__((always_inline)) {
+              o[0] = __uint_as_float(w << 16);
+              o[1] = __uint_as_float(w & 0xffff0000u);
+            };
+            if (a.accumulate) {  // out-of-range loads read zero
+              const u32x2 ok = __builtin_amdgcn_raw_buffer_load_b64(rk, voff, 0, 0);
+              const u32x2 ov = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, 0, 0);
+              float t[4];
+              unpack(ok[0], t), unpack(ok[1], t + 2);
+              for (int i = 0; i < 4; ++i) vk[i] += t[i];
+              unpack(ov[0], t), unpack(ov[1], t + 2);
+              for (int i = 0; i < 4; ++i) vv[i] += t[i];
             }
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vk[0], vk[1]), pack(vk[2], vk[3])}, rk, voff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vv[0], vv[1]), pack(vv[2], vv[3])}, rv, voff, 0, 0);
+          } else {
+            if (a.accumulate) {
+              const u32x4 ok = __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0);
+              const u32x4 ov = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0);
+              for (int i = 0; i < 4; ++i) {
+                vk[i] += __uint_as_float(ok[i]);
+                vv[i] += __uint_as_float(ov[i]);
+              }
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vk[0]), __float_as_uint(vk[1]), __float_as_uint(vk[2]), __float_as_uint(vk[3])}, rk, voff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vv[0]), __float_as_uint(vv[1]), __float_as_uint(vv[2]), __float_as_uint(vv[3])}, rv, voff, 0, 0);
           }
-          __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vk[0]), __float_as_uint(vk[1]), __float_as_uint(vk[2]), __float_as_uint(vk[3])}, rk, voff, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vv[0]), __float_as_uint(vv[1]), __float_as_uint(vv[2]), __float_as_uint(vv[3])}, rv, voff, 0, 0);
         }
       }
     }

@@ -538,35 +538,18 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
   if (slice_bytes < ((int64_t)1 << 31)) {
     const auto rk = make_rsrc(static_cast<const char*>(a.dK) + slice0 * esz, (uint32_t)slice_bytes);
     const auto rv = make_rsrc(static_cast<const char*>(a.dV) + slice0 * esz, (uint32_t)slice_bytes);
-    // Rows 4j..4j+3 of an accumulator are four consecutive keys, and the four
-    // lanes of a quad hold four consecutive d: a 4 x 4 transpose inside each
-    // quad (two DPP butterfly stages) leaves each lane four consecutive d of
-    // one key, stored with one 8-byte (bf16) or 16-byte (fp32) store.
-    const int q = l32 & 3;
-    auto xpose = [&](float v[4]) __attribute__((always_inline)) {
-#pragma unroll
-      for (int i = 0; i < 4; i += 2) {  // lane bit 0 <-> slot bit 0
-        const float send = (q & 1) ? v[i] : v[i + 1];
-        const float recv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
-        if (q & 1) v[i] = recv;
-        else v[i + 1] = recv;
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {  // lane bit 1 <-> slot bit 1
-        const float send = (q & 2) ? v[i] : v[i + 2];
-        const float recv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0x4E, 0xF, 0xF, false));
-        if (q & 2) v[i] = recv;
-        else v[i + 2] = recv;
-      }
+    // The accumulators leave through each wave's part of the idle stage
+    // buffer (free until the next item's first barrier; the next item's
+    // first tile loads into the other one), so that stores cover whole rows.
+    auto pack = [](float x, float y) __attribute__((always_inline)) {
+      return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
+             ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
     };
     if (a.grad_bf16 && !a.accumulate) {
-      // Overwritten bf16 gradients leave through LDS in whole rows: each
-      // wave writes its 32 keys' dK and dV (2 bytes per value, straight from
-      // the accumulators) into a row-major tile of its own in the idle stage
-      // buffer, 16-byte units XOR-swizzled by the row, then stores 16 bytes
-      // per lane, a store instruction covering 64 / U whole rows.  The next
-      // item's first tile loads into the other buffer, and this one is next
-      // written after the next item's first barrier.
+      // Overwritten bf16 gradients: each wave writes its 32 keys' dK and dV
+      // (2 bytes per value, straight from the accumulators) into a row-major
+      // tile of its own, 16-byte units XOR-swizzled by the row, then stores
+      // 16 bytes per lane, a store instruction covering 64 / U whole rows.
       constexpr int RB = 2 * D, U = RB / 16, RPI = 64 / U;
       static_assert(kWaves * 2 * 32 * RB <= C::kStageBytes, "dK and dV tiles of every wave fit a stage buffer");
       // An opaque zero in the tile address keeps its offsets from being
@@ -575,10 +558,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
       asm volatile("v_mov_b32 %0, 0" : "=v"(z));
       char* tile = bufB + wave * (2 * 32 * RB);  // dK rows, then dV rows
       auto at = [&](int row, int d) { return row * RB + 16 * ((d / 8) ^ (row & (U - 1))) + 2 * (d % 8); };
-      auto pack = [](float x, float y) __attribute__((always_inline)) {
-        return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
-               ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
-      };
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const int d = 32 * db + l32 + z;
@@ -606,56 +585,73 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{v4.x, v4.y, v4.z, v4.w}, rv, voff, 0, 0);
       }
     } else {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int d0 = 32 * db + (l32 & ~3);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float vk[4], vv[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            vk[i] = dk[db][4 * j + i] * a.scale;
-            vv[i] = dv[db][4 * j + i];
-          }
-          xpose(vk);  // all lanes take part in the exchange
-          xpose(vv);
-          if (d0 >= D) continue;  // whole quads (D is a multiple of 16)
-          const int kk = ekw0 + acc_row(4 * j, g) + q;
-          const int voff = (int)(((int64_t)kk * row_elems + d0) * esz);
+      // fp32 or accumulated gradients: dK, then dV, staged as fp32 rows in
+      // each wave's part of the idle stage buffer and read back 16 bytes
+      // (four values) per lane, added to the caller's values when
+      // accumulating, rounded once and stored as whole rows.
+      constexpr int RB = 4 * D, U = RB / 16, RPI = 64 / U;  // fp32 rows
+      static_assert(kWaves * 32 * RB <= C::kStageBytes, "a tensor's tiles of every wave fit a stage buffer");
+      int z;  // an opaque zero, as above
+      asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+      char* tile = bufB + wave * (32 * RB);
+      auto unit = [&](int row, int u) { return row * RB + 16 * (u ^ (row & (U - 1))); };
+      auto pass = [&](const f32x16* acc, float sc, const __amdgpu_buffer_rsrc_t& rs) __attribute__((always_inline)) {
+        constexpr int NI = 32 / RPI;
+        auto voff_of = [&](int i) {
+          const int row = i * RPI + (lane + z) / U, u = (lane + z) % U;
+          return (int)(((int64_t)(ekw0 + row) * row_elems + 4 * u) * esz);
+        };
+        // The caller's values, all requested before any is used (out-of-range
+        // loads read zero).
+        u32x2 old2[NI];  // bf16 gradients
+        u32x4 old4[NI];  // fp32 gradients
+        if (a.accumulate) {
           if (a.grad_bf16) {
-            auto pack = [](float x, float y) __attribute__((always_inline)) {
-              return (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(x)) |
-                     ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(y)) << 16);
-            };
-            auto unpack = [](uint32_t w, float* o) __attribute__((always_inline)) {
-              o[0] = __uint_as_float(w << 16);
-              o[1] = __uint_as_float(w & 0xffff0000u);
-            };
-            if (a.accumulate) {  // out-of-range loads read zero
-              const u32x2 ok = __builtin_amdgcn_raw_buffer_load_b64(rk, voff, 0, 0);
-              const u32x2 ov = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, 0, 0);
-              float t[4];
-              unpack(ok[0], t), unpack(ok[1], t + 2);
-              for (int i = 0; i < 4; ++i) vk[i] += t[i];
-              unpack(ov[0], t), unpack(ov[1], t + 2);
-              for (int i = 0; i < 4; ++i) vv[i] += t[i];
-            }
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vk[0], vk[1]), pack(vk[2], vk[3])}, rk, voff, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(vv[0], vv[1]), pack(vv[2], vv[3])}, rv, voff, 0, 0);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) old2[i] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff_of(i), 0, 0);
           } else {
-            if (a.accumulate) {
-              const u32x4 ok = __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0);
-              const u32x4 ov = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0);
-              for (int i = 0; i < 4; ++i) {
-                vk[i] += __uint_as_float(ok[i]);
-                vv[i] += __uint_as_float(ov[i]);
-              }
-            }
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vk[0]), __float_as_uint(vk[1]), __float_as_uint(vk[2]), __float_as_uint(vk[3])}, rk, voff, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(vv[0]), __float_as_uint(vv[1]), __float_as_uint(vv[2]), __float_as_uint(vv[3])}, rv, voff, 0, 0);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) old4[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff_of(i), 0, 0);
           }
         }
-      }
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int d = 32 * db + l32 + z;
+          if (d < D) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int row = acc_row(r, g) + z;
+              *reinterpret_cast<float*>(tile + unit(row, d / 4) + 4 * (d % 4)) = acc[db][r] * sc;
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int row = i * RPI + (lane + z) / U, u = (lane + z) % U;
+          const uint4 w = *reinterpret_cast<const uint4*>(tile + unit(row, u));
+          float v[4] = {__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w)};
+          const int voff = voff_of(i);
+          if (a.grad_bf16) {
+            if (a.accumulate) {
+              v[0] += __uint_as_float(old2[i][0] << 16);
+              v[1] += __uint_as_float(old2[i][0] & 0xffff0000u);
+              v[2] += __uint_as_float(old2[i][1] << 16);
+              v[3] += __uint_as_float(old2[i][1] & 0xffff0000u);
+            }
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack(v[0], v[1]), pack(v[2], v[3])}, rs, voff, 0, 0);
+          } else {
+            if (a.accumulate) {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) v[k] += __uint_as_float(old4[i][k]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])}, rs, voff,
+                0, 0);
+          }
+        }
+      };
+      pass(dk, a.scale, rk);
+      pass(dv, 1.0f, rv);
     }
   } else {
 #pragma unroll

@@ -977,9 +977,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
       constexpr int EPL = 16 / (int)sizeof(E);  // output elements per lane
       constexpr int LPR = D / EPL;              // lanes per row
       constexpr int RPI = 64 / LPR;             // rows per instruction
+      constexpr int NI = 32 / RPI;
       E* base = static_cast<E*>(a.dQ) + ((int64_t)b * T * a.H + h) * D;
+      // When accumulating, the caller's values are all requested before the
+      // first is used (rows past T read the wave's first row, unused).
+      uint4 old[NI];
+      if (a.accumulate) {
 #pragma unroll
-      for (int i = 0; i < 32 / RPI; ++i) {
+        for (int i = 0; i < NI; ++i) {
+          const int row = i * RPI + lane / LPR, e0 = EPL * (lane % LPR);
+          const int qr = q0w + row < T ? q0w + row : q0w;
+          old[i] = *reinterpret_cast<const uint4*>(base + (int64_t)qr * a.H * D + e0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
         const int row = i * RPI + lane / LPR, e0 = EPL * (lane % LPR);
         float v[EPL];
 #pragma unroll
@@ -991,8 +1003,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
         if (q0w + row < T) {
           E* p = base + (int64_t)(q0w + row) * a.H * D + e0;
           if (a.accumulate) {
-            const uint4 old = *reinterpret_cast<const uint4*>(p);
-            const E* o = reinterpret_cast<const E*>(&old);
+            const E* o = reinterpret_cast<const E*>(&old[i]);
 #pragma unroll
             for (int k = 0; k < EPL; ++k) v[k] += to_f32(o[k]);
           }

@@ -405,9 +405,9 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=16, help="batch rows in the CPU baseline sample")
     ap.add_argument("--configs", default="C1,C2,C4,C5",
                     help="other BASELINE workloads timed beside the headline (comma list; '' for none)")
-    ap.add_argument("--sections", default="prologue,loss,optim",
-                    help="measurements besides the headline attention step (comma list of prologue, loss, optim; "
-                         "'none' for only the headline)")
+    ap.add_argument("--sections", default="accumulate,prologue,loss,optim",
+                    help="measurements besides the headline attention step (comma list of accumulate, prologue, "
+                         "loss, optim; 'none' for only the headline)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this build has a single MI355X, and the attention "
@@ -448,11 +448,14 @@ def main() -> int:
 
     # The headline workload once more with the reference's default backward
     # semantics (gradients added to the buffers' values, src/kernels.jl:420).
-    acc = measure_attention(wl, dev, args.steps, args.warmup, accumulate=True)
-    accumulated = {"ms_per_step": acc["ms_per_step"], "tflops": acc["tflops"], "peak_frac": acc["peak_frac"],
-                   "kernels": {k: v["avg_ms"] for k, v in acc["kernels"].items()}}
+    requested = set(args.sections.split(","))
+    accumulated = None
+    if "accumulate" in requested:
+        acc = measure_attention(wl, dev, args.steps, args.warmup, accumulate=True)
+        accumulated = {"ms_per_step": acc["ms_per_step"], "tflops": acc["tflops"], "peak_frac": acc["peak_frac"],
+                       "kernels": {k: v["avg_ms"] for k, v in acc["kernels"].items()}}
 
-    sections = set(args.sections.split(",")) if fast else set()
+    sections = requested if fast else set()
     prologue = measure_prologue(wl, dev, args.steps) if "prologue" in sections else None
     loss_side = measure_loss(dev, args.steps) if "loss" in sections else None
     optim_side = measure_optim(dev, args.steps) if "optim" in sections else None

@@ -28,10 +28,9 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-# Per-source additions.  The bf16 forward takes row maxima of MFMA results;
-# with NaNs ruled out the compiler drops the canonicalising max it otherwise
-# puts in front of every comparison.  Its inputs carry no NaN by contract.
-EXTRA_FLAGS = {"attn_fwd_fast.hip": ["-fno-honor-nans"]}
+# Per-source additions (none at present; every source builds with the flags
+# above, IEEE NaN semantics included).
+EXTRA_FLAGS = {}
 
 
 def hipcc() -> str:

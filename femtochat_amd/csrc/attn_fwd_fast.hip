@@ -74,9 +74,9 @@ __device__ inline void mask_block(f32x16& s, int k0, int g, int lb, int ub) {
   }
 }
 
-// Maxima propagate NaN, as Julia's max does: llvm.maximum is one
-// v_maximum3_f32 per two new values and needs no canonicalising v_max_f32 on
-// MFMA results, where fmaxf costs three instructions per two values.
+// Maxima propagate NaN, as Julia's max does: llvm.maximum compiles to one
+// v_maximum3_f32 per two new values and, unlike fmaxf, needs no canonicalising
+// v_max_f32 in front of MFMA results.
 __device__ inline float nan_max(float x, float y) { return __builtin_elementwise_maximum(x, y); }
 
 __device__ inline float max16(const f32x16& s) {

@@ -431,3 +431,31 @@ def test_fast_forward_large_logit_growth(gpu, growth):
         e = rel_err(to_np(x), r)
         say(f"  {name} rel err {e:.2e}")
         assert e <= TOL["fast"], name
+
+
+@pytest.mark.parametrize("mode", ["exact", "fast"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_nan_query_stays_in_its_row(gpu, mode, D):
+    # A NaN in one query makes that query's scores NaN.  The reference's
+    # maximum, exp and sums carry it (Julia's max propagates NaN), so that row's
+    # O and log-sum-exp are NaN; the other queries never see it and must match
+    # the oracle on the clean input.
+    fast = mode == "fast"
+    B, T, H, Hkv = 1, 200, 2, 1
+    bad_t, bad_h = 150, 1
+    Q, K, V, _ = _inputs(11 + D, B, T, H, Hkv, D, fast)
+    Qn = Q.copy()
+    Qn[0, bad_t, bad_h, 3] = np.nan
+    Qd, Kd, Vd = (_dev(x, fast, gpu) for x in (Qn, K, V))
+    say(f"case NaN query mode={mode} D={D} at t={bad_t} h={bad_h}")
+    O, l, m = gpu_forward(MFMAFast() if fast else MFMAExact(), Qd, Kd, Vd, (-1, 0))
+    torch.cuda.synchronize()
+    O, l, m = to_np(O).copy(), to_np(l).copy(), to_np(m).copy()
+    assert np.all(np.isnan(O[0, bad_t, bad_h])), "the NaN query's output row must be NaN"
+    assert np.isnan(l[0, bad_h, bad_t]) or np.isnan(m[0, bad_h, bad_t]), "its log-sum-exp must be NaN"
+    O_ref, l_ref, m_ref = R.forward(Q, K, V, (-1, 0))
+    O[0, bad_t, bad_h] = O_ref[0, bad_t, bad_h]
+    l[0, bad_h, bad_t], m[0, bad_h, bad_t] = l_ref[0, bad_h, bad_t], m_ref[0, bad_h, bad_t]
+    assert np.all(np.isfinite(O)) and np.all(np.isfinite(l))
+    assert rel_err(O, O_ref) <= TOL[mode]
+    assert lse_err(l, m, l_ref, m_ref) <= TOL_LSE

@@ -99,3 +99,15 @@ def test_python_mirror_rejects_bad_arguments_before_the_library():
 def test_geometry_keywords_are_accepted():
     # scripts/train.jl:26 passes backward=(; warps=Val(4), query_tile=Val(64)).
     Kn._reject_unknown({"warps": 4, "query_tile": 64, "head_span": 1})
+
+
+def test_build_flags_keep_ieee_nan_and_packed_fp32_off():
+    # Every HIP source builds with IEEE NaN semantics (a NaN query must reach
+    # its own row's outputs, as Julia's max and exp carry it) and with packed
+    # FP32 instructions disabled for the device code.
+    from femtochat_amd import build as B
+    flags = list(B.HIPCC_FLAGS) + [f for extra in B.EXTRA_FLAGS.values() for f in extra]
+    for bad in ("-ffast-math", "-fno-honor-nans", "-ffinite-math-only", "-funsafe-math-optimizations"):
+        assert bad not in flags, bad
+    seq = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+    assert any(flags[i:i + 4] == seq for i in range(len(flags) - 3))

@@ -980,13 +980,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
       constexpr int NI = 32 / RPI;
       E* base = static_cast<E*>(a.dQ) + ((int64_t)b * T * a.H + h) * D;
       // When accumulating, the caller's values are all requested before the
-      // first is used (rows past T read the wave's first row, unused).
+      // first is used (rows past T read the slice's last row, unused).
       uint4 old[NI];
       if (a.accumulate) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           const int row = i * RPI + lane / LPR, e0 = EPL * (lane % LPR);
-          const int qr = q0w + row < T ? q0w + row : q0w;
+          const int qr = epilogue_row(q0w, row, T);
           old[i] = *reinterpret_cast<const uint4*>(base + (int64_t)qr * a.H * D + e0);
         }
       }

@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
     ordered_query_item(blockIdx.x, a.order, n_qt, a.H, a.Hkv, a.group, b, h, qt);
   } else if (a.local_order) {
     // Query tiles from ceil(left / BM) on see a whole window.
-    local_query_item(blockIdx.x, (int)gridDim.x, n_qt, min(n_qt, (a.left + C::kBM - 1) / C::kBM), a.B, a.Hkv,
+    local_query_item(blockIdx.x, (int)gridDim.x, n_qt, local_full_from(n_qt, a.left, C::kBM), a.B, a.Hkv,
                      a.group, b, h, qt);
   } else {
     const GridItem it0 = heavy_first(blockIdx.x, a.H * a.B);

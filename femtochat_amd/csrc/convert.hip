@@ -92,6 +92,13 @@ fc_status fc_convert(const void* src, int32_t src_dtype, void* dst, int32_t dst_
   const size_t esrc = src_dtype == FC_BF16 ? 2 : 4, edst = dst_dtype == FC_BF16 ? 2 : 4;
   if ((reinterpret_cast<uintptr_t>(src) & (esrc - 1)) != 0 || (reinterpret_cast<uintptr_t>(dst) & (edst - 1)) != 0)
     return fc::set_error(FC_ERR_INVALID_ARGUMENT, "fc_convert: pointers must be aligned to their element size");
+  // The kernels read and write through restrict pointers: a thread may write
+  // bytes that another is still to read unless each element maps onto itself.
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
+  const bool overlap = s0 < d0 + (uintptr_t)n * edst && d0 < s0 + (uintptr_t)n * esrc;
+  if (overlap && !(s0 == d0 && src_dtype == dst_dtype))
+    return fc::set_error(FC_ERR_INVALID_ARGUMENT,
+                         "fc_convert: source and destination overlap (allowed only when equal with equal dtypes)");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const fc::ProfileMark mk = fc::profile_begin(s);
   int64_t done = 0;

@@ -175,7 +175,10 @@ fc_status fc_rope_norm_bwd(const fc_rope_norm_desc* desc, const void* dY,
  * for the tensor-core path (reference ext/FemtoChatCUDAExt.jl:229-230, there
  * to Float16) and the Float32.(x) of a bf16 result, so a binding converts
  * without GPU code of its own.  Pointers must be aligned to their element
- * size; the source and destination must not overlap unless equal. */
+ * size; the source and destination must not overlap, except that equal
+ * pointers with equal dtypes (an in-place copy) are allowed: any other
+ * overlap, including src == dst with different dtypes, returns
+ * FC_ERR_INVALID_ARGUMENT. */
 fc_status fc_convert(const void* src, int32_t src_dtype, void* dst,
                      int32_t dst_dtype, int64_t n, void* stream);
 

@@ -4,6 +4,7 @@
 // every entry point runs on the host before a launch), and the float32 FA-1
 // restatement oracle/fa1.c on ragged shapes, checked against a direct float64
 // softmax attention.
+#include "../../femtochat_amd/csrc/attn_index.hpp"
 #include "../../femtochat_amd/csrc/attn_problem.hpp"
 
 #include <cmath>
@@ -169,8 +170,57 @@ static void restatement(int D, int H, int Hkv, int T, int B, int left, int right
   CHECK(err <= 1e-5 * scale);
 }
 
+// The row-local grid order of the fast forward (local_query_item with
+// local_full_from, as attn_fwd_fast.hip calls them) must name every
+// (batch, head, tile) item exactly once, with every index in range, for any
+// window the descriptor accepts (left clamped to [-T-1, T]; a window that
+// starts right of the query has left < 0).
+static void grid_orders() {
+  const int BM = 128;
+  struct Shape { int B, Hkv, group, T; };
+  const Shape shapes[] = {{16, 5, 2, 2048}, {2, 4, 2, 1000}, {3, 3, 1, 777}, {8, 1, 4, 300}, {1, 2, 3, 129}};
+  for (const Shape& sh : shapes) {
+    const int n_qt = (sh.T + BM - 1) / BM, H = sh.Hkv * sh.group, n_items = n_qt * H * sh.B;
+    const int lefts[] = {-sh.T - 1, -300, -255, -256, -128, -127, -1, 0, 1, 127, 128, 129, 512, sh.T / 2, sh.T};
+    for (int left : lefts) {
+      const int full_from = fc::local_full_from(n_qt, left, BM);
+      CHECK(full_from >= 0 && full_from <= n_qt);
+      std::vector<int> seen((size_t)n_items, 0);
+      bool in_range = true;
+      for (int id = 0; id < n_items; ++id) {
+        int b = -1, h = -1, tile = -1;
+        fc::local_query_item(id, n_items, n_qt, full_from, sh.B, sh.Hkv, sh.group, b, h, tile);
+        if (b < 0 || b >= sh.B || h < 0 || h >= H || tile < 0 || tile >= n_qt) {
+          in_range = false;
+          continue;
+        }
+        ++seen[((size_t)b * H + h) * n_qt + tile];
+      }
+      CHECK(in_range);
+      bool once = true;
+      for (int c : seen) once = once && c == 1;
+      if (!in_range || !once)
+        std::fprintf(stderr, "local order B=%d Hkv=%d group=%d T=%d left=%d is not a bijection\n", sh.B, sh.Hkv,
+                     sh.group, sh.T, left);
+      CHECK(once);
+    }
+  }
+  // The accumulate epilogue's row for every lane of every wave: inside the
+  // slice for ragged T, and the lane's own row whenever that row exists.
+  for (int T : {1, 31, 32, 33, 129, 150, 777, 2000, 2048}) {
+    const int n_waves = (T + 127) / 128 * 4;
+    for (int w = 0; w < n_waves; ++w)
+      for (int row = 0; row < 32; ++row) {
+        const int q0 = 32 * w, r = fc::epilogue_row(q0, row, T);
+        CHECK(r >= 0 && r < T);
+        if (q0 + row < T) CHECK(r == q0 + row);
+      }
+  }
+}
+
 int main() {
   validation();
+  grid_orders();
   restatement(16, 2, 1, 37, 2, -1, 0, 1, false);
   restatement(32, 4, 2, 600, 1, 100, 0, 0, false);  // two key blocks, a ragged one
   restatement(16, 2, 2, 530, 1, 50, 20, 0, true);

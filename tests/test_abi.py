@@ -107,6 +107,26 @@ def test_null_descriptor_and_pointers():
     assert st == L.FC_ERR_INVALID_ARGUMENT
 
 
+def test_convert_rejects_overlapping_buffers():
+    """fc_convert runs restrict-qualified kernels: any overlap other than an
+    in-place copy of one dtype is rejected on the host (no launch)."""
+    lib = L.lib()
+    base = 0x100000
+    n = 1024
+    # in place with different dtypes: thread i would write bytes thread i/2 still reads
+    for sd, dd in ((L.FC_F32, L.FC_BF16), (L.FC_BF16, L.FC_F32)):
+        st = lib.fc_convert(ctypes.c_void_p(base), sd, ctypes.c_void_p(base), dd, ctypes.c_int64(n), None)
+        assert st == L.FC_ERR_INVALID_ARGUMENT
+        assert "overlap" in lib.fc_last_error().decode()
+    # partial overlap, equal dtypes
+    st = lib.fc_convert(ctypes.c_void_p(base), L.FC_F32, ctypes.c_void_p(base + 64), L.FC_F32, ctypes.c_int64(n), None)
+    assert st == L.FC_ERR_INVALID_ARGUMENT
+    # a bf16 destination just below an fp32 source of the same count, one byte into it
+    st = lib.fc_convert(ctypes.c_void_p(base + 2 * n - 2), L.FC_F32, ctypes.c_void_p(base), L.FC_BF16,
+                        ctypes.c_int64(n), None)
+    assert st == L.FC_ERR_INVALID_ARGUMENT
+
+
 def test_workspace_checks():
     lib = L.lib()
     d = desc()

@@ -104,6 +104,16 @@ def test_small_cases(gpu, case):
     _check_case(gpu, mode, B, T, H, Hkv, D, window, seed=zlib.crc32(repr(case).encode()) % 1000)
 
 
+@pytest.mark.parametrize("window", [(-300, 400), (-255, 300), (-701, 700)])
+def test_window_right_of_query_row_local_order(gpu, window):
+    """Windows that start right of their query (left <= -255) in fast mode, with
+    B*Hkv = 16 (a multiple of 8) and left + right + 1 <= T/2, so the forward
+    and dK/dV take the row-local order: every query tile must be computed
+    exactly once (the first full tile clamps to 0 for left < 0).  (-701, 700)
+    at T = 700 leaves every row empty (left clamps to -T-1)."""
+    _check_case(gpu, "fast", 4, 700, 4, 4, 64, window, seed=abs(window[0]))
+
+
 @pytest.mark.parametrize("mode", ["exact", "fast"])
 @pytest.mark.parametrize("T,D,window", [(300, 64, (-1, 0)), (517, 128, (100, 0)), (260, 128, (-1, 0))])
 def test_document_mask(gpu, mode, T, D, window):

@@ -162,19 +162,43 @@ fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, co
     return fail(FC_ERR_INVALID_ARGUMENT, "fc_attn_fwd: a required pointer is null");
   p.positions = positions != nullptr;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // The workspace is optional: with one, fast mode with positions takes the
-  // query tiles in the work order.
+  // The workspace is optional unless the head dim runs padded: with one,
+  // fast mode with positions takes the query tiles in the work order.
   const fc::FwdWorkspace ws = fc::fwd_workspace(p);
-  int32_t* order = nullptr;
-  if (ws.total > 0 && workspace != nullptr) {
-    if (workspace_bytes < ws.total)
-      return fail(FC_ERR_WORKSPACE, "forward workspace needs %zu bytes, got %zu", ws.total, workspace_bytes);
+  char* w = nullptr;
+  if (ws.total > 0 && (workspace != nullptr || fc::padded(p))) {
+    if (workspace == nullptr || workspace_bytes < ws.total)
+      return fail(FC_ERR_WORKSPACE, "forward workspace needs %zu bytes, got %zu%s", ws.total, workspace_bytes,
+                  fc::padded(p) ? " (head_dim runs on padded copies)" : "");
     if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
       return fail(FC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-    char* w = static_cast<char*>(workspace);
+    w = static_cast<char*>(workspace);
+  }
+  hipError_t e = hipSuccess;
+  // A non-compiled head dim: Q, K, V copied into rows of Dk values, zero
+  // beyond D, and O written there first.
+  const fc::PadWorkspace pw = fc::pad_workspace(p, false);
+  void* Ok = O;
+  if (fc::padded(p)) {
+    const int64_t rq = (int64_t)p.B * p.T * p.H, rk = (int64_t)p.B * p.T * p.Hkv;
+    const int in16 = p.bf16 ? 1 : 0;
+    const fc::RepackArgs packs[3] = {{Q, w + pw.Q, rq, p.D, p.Dk, in16, in16, 0},
+                                     {K, w + pw.K, rk, p.D, p.Dk, in16, in16, 0},
+                                     {V, w + pw.V, rk, p.D, p.Dk, in16, in16, 0}};
+    for (const fc::RepackArgs& r : packs) {
+      e = fc::launch_repack(r, s);
+      if (e != hipSuccess) return fail(FC_ERR_HIP, "padding launch failed: %s", hipGetErrorString(e));
+    }
+    Q = w + pw.Q;
+    K = w + pw.K;
+    V = w + pw.V;
+    Ok = w + pw.O;
+  }
+  int32_t* order = nullptr;
+  if (fc::ordered(p) && w != nullptr) {
     int32_t* chunk_lb = reinterpret_cast<int32_t*>(w + ws.chunk_lb);
     order = reinterpret_cast<int32_t*>(w + ws.qorder);
-    hipError_t e = fc::launch_bounds(p, fc::BoundsArgs{positions, chunk_lb, p.T, p.B, p.left}, s);
+    e = fc::launch_bounds(p, fc::BoundsArgs{positions, chunk_lb, p.T, p.B, p.left}, s);
     if (e != hipSuccess) return fail(FC_ERR_HIP, "bounds launch failed: %s", hipGetErrorString(e));
     e = fc::launch_order(p, fc::OrderArgs{chunk_lb, order, nullptr, p.T, p.B, p.left, p.right}, s);
     if (e != hipSuccess) return fail(FC_ERR_HIP, "order launch failed: %s", hipGetErrorString(e));
@@ -186,7 +210,7 @@ fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, co
   a.pos = positions;
   a.order = order;
   a.local_order = fc::windowed(p) ? 1 : 0;
-  a.O = O;
+  a.O = Ok;
   a.l = l;
   a.m = m;
   a.H = p.H;
@@ -198,8 +222,13 @@ fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K, co
   a.right = p.right;
   a.out_bf16 = p.out_bf16 ? 1 : 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)p.D));
-  const hipError_t e = fc::launch_fwd(p, a, s);
+  e = fc::launch_fwd(p, a, s);
   if (e != hipSuccess) return fail(FC_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
+  if (fc::padded(p)) {
+    const int o16 = p.out_bf16 ? 1 : 0;
+    e = fc::launch_repack(fc::RepackArgs{Ok, O, (int64_t)p.B * p.T * p.H, p.Dk, p.D, o16, o16, 0}, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "unpadding launch failed: %s", hipGetErrorString(e));
+  }
   return ok();
 }
 
@@ -317,6 +346,42 @@ fc_status bwd_launch(const fc::Problem& p, const void* dO, const void* Q, const 
   return ok();
 }
 
+// The backward of a validated problem: bwd_launch directly for a compiled
+// head dim; otherwise the inputs are copied into rows of Dk values (zero
+// beyond D), the kernels overwrite float32 gradients of that width, and
+// their first D columns are added to (or written into) the caller's
+// gradients, rounded once.
+fc_status bwd_run(const fc::Problem& p, const void* dO, const void* Q, const void* K, const void* V,
+                  const void* O, const float* l, const float* m, const int32_t* positions, void* dQ, void* dK,
+                  void* dV, char* w, hipStream_t s) {
+  if (!fc::padded(p)) return bwd_launch(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, w, s);
+  const fc::PadWorkspace pw = fc::pad_workspace(p, true);
+  const int64_t rq = (int64_t)p.B * p.T * p.H, rk = (int64_t)p.B * p.T * p.Hkv;
+  const int in16 = p.bf16 ? 1 : 0, o16 = p.out_bf16 ? 1 : 0, do16 = p.dout_bf16 ? 1 : 0;
+  const fc::RepackArgs packs[5] = {{Q, w + pw.Q, rq, p.D, p.Dk, in16, in16, 0},
+                                   {K, w + pw.K, rk, p.D, p.Dk, in16, in16, 0},
+                                   {V, w + pw.V, rk, p.D, p.Dk, in16, in16, 0},
+                                   {O, w + pw.O, rq, p.D, p.Dk, o16, o16, 0},
+                                   {dO, w + pw.dO, rq, p.D, p.Dk, do16, do16, 0}};
+  for (const fc::RepackArgs& r : packs) {
+    const hipError_t e = fc::launch_repack(r, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "padding launch failed: %s", hipGetErrorString(e));
+  }
+  const fc::Problem k = fc::kernel_problem(p, true);
+  const fc_status st = bwd_launch(k, w + pw.dO, w + pw.Q, w + pw.K, w + pw.V, w + pw.O, l, m, positions, w + pw.dQ,
+                                  w + pw.dK, w + pw.dV, w, s);
+  if (st != FC_OK) return st;
+  const int g16 = p.grad_bf16 ? 1 : 0, acc = p.accumulate ? 1 : 0;
+  const fc::RepackArgs unpacks[3] = {{w + pw.dQ, dQ, rq, p.Dk, p.D, 0, g16, acc},
+                                     {w + pw.dK, dK, rk, p.Dk, p.D, 0, g16, acc},
+                                     {w + pw.dV, dV, rk, p.Dk, p.D, 0, g16, acc}};
+  for (const fc::RepackArgs& r : unpacks) {
+    const hipError_t e = fc::launch_repack(r, s);
+    if (e != hipSuccess) return fail(FC_ERR_HIP, "unpadding launch failed: %s", hipGetErrorString(e));
+  }
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -333,8 +398,8 @@ fc_status fc_attn_bwd(const fc_attn_desc* desc, const void* dO, const void* Q, c
                 workspace == nullptr ? " (null)" : "");
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
     return fail(FC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  return bwd_launch(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, static_cast<char*>(workspace),
-                    static_cast<hipStream_t>(stream));
+  return bwd_run(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, static_cast<char*>(workspace),
+                 static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"
@@ -393,7 +458,7 @@ fc_status fc_attn_bwd_noalloc(const fc_attn_desc* desc, const void* dO, const vo
   char* w = nullptr;
   st = current_scratch(&w);
   if (st != FC_OK) return st;
-  return bwd_launch(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, w, static_cast<hipStream_t>(stream));
+  return bwd_run(p, dO, Q, K, V, O, l, m, positions, dQ, dK, dV, w, static_cast<hipStream_t>(stream));
 }
 
 // ---- attention prologue (rope_norm.hip) -----------------------------------

@@ -612,7 +612,7 @@ static hipError_t launch_pre_d(const Problem& p, const PreArgs& a, hipStream_t s
 }
 
 hipError_t launch_bwd_pre(const Problem& p, const PreArgs& a, hipStream_t s) {
-  switch (p.D) {
+  switch (p.Dk) {
     case 16: return launch_pre_d<16>(p, a, s);
     case 32: return launch_pre_d<32>(p, a, s);
     case 64: return launch_pre_d<64>(p, a, s);
@@ -663,7 +663,7 @@ static hipError_t launch_dq_t(const Problem& p, const BwdArgs& a, hipStream_t s)
 }
 
 #define FC_DISPATCH_D(FN, E)                       \
-  switch (p.D) {                                   \
+  switch (p.Dk) {                                   \
     case 16: return FN<E, 16>(p, a, s);            \
     case 32: return FN<E, 32>(p, a, s);            \
     case 64: return FN<E, 64>(p, a, s);            \

@@ -1050,7 +1050,7 @@ static hipError_t launch_dq_fast_t(const Problem& p, const BwdArgs& a, hipStream
 }
 
 hipError_t launch_bwd_dkdv_fast(const Problem& p, const BwdArgs& a, hipStream_t s) {
-  switch (p.D) {
+  switch (p.Dk) {
     case 16: return launch_dkdv_fast_t<16>(p, a, s);
     case 32: return launch_dkdv_fast_t<32>(p, a, s);
     case 64: return launch_dkdv_fast_t<64>(p, a, s);
@@ -1060,7 +1060,7 @@ hipError_t launch_bwd_dkdv_fast(const Problem& p, const BwdArgs& a, hipStream_t 
 }
 
 hipError_t launch_bwd_dq_fast(const Problem& p, const BwdArgs& a, hipStream_t s) {
-  switch (p.D) {
+  switch (p.Dk) {
     case 16: return launch_dq_fast_t<16>(p, a, s);
     case 32: return launch_dq_fast_t<32>(p, a, s);
     case 64: return launch_dq_fast_t<64>(p, a, s);

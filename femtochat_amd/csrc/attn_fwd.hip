@@ -225,7 +225,7 @@ static hipError_t launch_fwd_t(const Problem& p, const FwdArgs& a, hipStream_t s
 
 template <typename E>
 static hipError_t launch_fwd_e(const Problem& p, const FwdArgs& a, hipStream_t s) {
-  switch (p.D) {
+  switch (p.Dk) {
     case 16: return launch_fwd_t<E, 16>(p, a, s);
     case 32: return launch_fwd_t<E, 32>(p, a, s);
     case 64: return launch_fwd_t<E, 64>(p, a, s);

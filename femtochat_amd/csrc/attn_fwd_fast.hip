@@ -468,7 +468,7 @@ static hipError_t launch_fwd_fast_t(const Problem& p, const FwdArgs& a, hipStrea
 }
 
 hipError_t launch_fwd_fast(const Problem& p, const FwdArgs& a, hipStream_t s) {
-  switch (p.D) {
+  switch (p.Dk) {
     case 16: return launch_fwd_fast_t<16>(p, a, s);
     case 32: return launch_fwd_fast_t<32>(p, a, s);
     case 64: return launch_fwd_fast_t<64>(p, a, s);

@@ -168,6 +168,19 @@ struct EmbedSortLayout {
 EmbedSortLayout embed_sort_layout(int64_t N, int vocab);
 hipError_t launch_embed_sorted(const EmbedArgs& a, bool bf16_dy, void* workspace, hipStream_t s);
 
+// Row repacking between head dims (convert.hip): rows of src_cols values
+// into rows of dst_cols values, zero-filled or truncated, optionally added
+// to the destination's values (fp32, one rounding).
+struct RepackArgs {
+  const void* src;
+  void* dst;
+  int64_t rows;
+  int src_cols, dst_cols;
+  int src_bf16, dst_bf16;
+  int accumulate;
+};
+hipError_t launch_repack(const RepackArgs& a, hipStream_t s);
+
 // Compute units of the current device (cached per device).
 hipError_t device_cus(int* cus);
 

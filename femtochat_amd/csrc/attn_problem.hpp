@@ -16,7 +16,9 @@ namespace fc {
 // Normalised problem: window already mapped to (left,right) with the causal
 // sentinel (-1,0) replaced by (T,0) and both extents clamped to [-T-1, T].
 struct Problem {
-  int D, H, Hkv, T, B, group;
+  int D;   // the caller's head dim (the scale is 1/sqrt(D))
+  int Dk;  // the head dim the kernels run with: D, or the compiled width D is zero-padded to
+  int H, Hkv, T, B, group;
   int left, right;
   bool bf16;        // fast mode (bf16 inputs) vs exact mode (fp32)
   bool out_bf16;    // O storage
@@ -55,8 +57,13 @@ inline bool windowed(const Problem& p) {
   return p.bf16 && !p.positions && (int64_t)p.left + std::max(p.right, 0) + 1 <= p.T / 2;
 }
 
-// Head dims the kernels are compiled for.
-inline bool head_dim_supported(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+// Head dims the kernels are compiled for; every other multiple of 16 up to
+// 128 runs on copies zero-padded to the next of them (a zero column adds
+// nothing to Q.K, dO.V or dO.O, and the padded output columns are dropped).
+inline bool head_dim_compiled(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+inline bool head_dim_supported(int D) { return D >= 16 && D <= 128 && D % 16 == 0; }
+inline int kernel_head_dim(int D) { return D <= 16 ? 16 : D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+inline bool padded(const Problem& p) { return p.Dk != p.D; }
 
 inline bool valid_dtype(int32_t d) { return d == FC_F32 || d == FC_BF16; }
 
@@ -84,12 +91,9 @@ inline fc_status make_problem(const fc_attn_desc* d, Problem* p, char* msg, size
     snprintf(msg, msg_len, "head_dim %d must be a multiple of 16 and at most 128", d->D);
     return FC_ERR_INVALID_ARGUMENT;
   }
-  if (!head_dim_supported(d->D)) {
-    snprintf(msg, msg_len, "head_dim %d is not compiled in (supported: 16, 32, 64, 128)", d->D);
-    return FC_ERR_UNSUPPORTED;
-  }
   const int64_t rows = (int64_t)d->B * d->T * d->H;
-  if (rows * d->D >= (int64_t)1 << 40 || rows > INT32_MAX / 2) return bad(FC_ERR_UNSUPPORTED, "problem too large");
+  if (rows * kernel_head_dim(d->D) >= (int64_t)1 << 40 || rows > INT32_MAX / 2)
+    return bad(FC_ERR_UNSUPPORTED, "problem too large");
   if (!valid_dtype(d->in_dtype) || !valid_dtype(d->out_dtype) || !valid_dtype(d->dout_dtype) ||
       !valid_dtype(d->grad_dtype))
     return bad(FC_ERR_INVALID_ARGUMENT, "dtype codes must be FC_F32 or FC_BF16");
@@ -101,8 +105,8 @@ inline fc_status make_problem(const fc_attn_desc* d, Problem* p, char* msg, size
       return bad(FC_ERR_INVALID_ARGUMENT, "fast mode takes bfloat16 Q/K/V (convert first, as attention_inputs does)");
     // The fast kernels read a (batch, head) slice through one buffer
     // descriptor with 32-bit offsets.
-    if (fast_slice_bytes(d->T, d->H, d->D) >= ((int64_t)1 << 31) ||
-        fast_slice_bytes(d->T, d->Hkv, d->D) >= ((int64_t)1 << 31)) {
+    const int Dk = kernel_head_dim(d->D);
+    if (fast_slice_bytes(d->T, d->H, Dk) >= ((int64_t)1 << 31) || fast_slice_bytes(d->T, d->Hkv, Dk) >= ((int64_t)1 << 31)) {
       snprintf(msg, msg_len, "fast mode: a (batch, head) slice of T*H*D = %lld bf16 values spans 2^31 bytes or more",
                (long long)d->T * d->H * d->D);
       return FC_ERR_UNSUPPORTED;
@@ -117,6 +121,7 @@ inline fc_status make_problem(const fc_attn_desc* d, Problem* p, char* msg, size
   }
 
   p->D = d->D;
+  p->Dk = kernel_head_dim(d->D);
   p->H = d->H;
   p->Hkv = d->Hkv;
   p->T = d->T;
@@ -142,16 +147,64 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline size_t chunk_bounds_bytes(const Problem& p) { return (size_t)p.B * ((p.T + 31) / 32) * 2 * sizeof(int32_t); }
 inline size_t order_bytes(const Problem& p) { return (size_t)p.B * ((p.T + kOrderRows - 1) / kOrderRows) * sizeof(int32_t); }
 
-// Workspace layout of the forward pass (byte offsets, 256-aligned): empty
-// unless the work order applies, then the per-32-query key bounds and the
-// query tiles' order.  The forward runs without it too (default order).
+// Workspace layout of the forward pass (byte offsets, 256-aligned): the
+// padded copies of a non-compiled head dim (required then), and when the
+// work order applies the per-32-query key bounds and the query tiles' order
+// (optional: the forward of a compiled head dim runs without a workspace,
+// in the default order).
 struct FwdWorkspace {
   size_t chunk_lb, qorder, total;
 };
 
+// The problem the kernels run: a padded problem's head dim replaced by the
+// compiled width (the scale still follows p.D).  A padded backward runs with
+// float32 gradients that it overwrites; they are added to (or written into)
+// the caller's gradients afterwards, rounded once.
+inline Problem kernel_problem(const Problem& p, bool backward) {
+  Problem k = p;
+  if (padded(p) && backward) {
+    k.grad_bf16 = false;
+    k.accumulate = false;
+  }
+  return k;
+}
+
+// Padded copies of a non-compiled head dim (byte offsets, 256-aligned):
+// Q, K, V (input format), O (its format), and in the backward dO (its
+// format) and float32 dQ, dK, dV, all with rows of Dk values.  The kernels'
+// own workspace of the padded problem follows at `inner`.
+struct PadWorkspace {
+  size_t Q, K, V, O, dO, dQ, dK, dV, inner;
+};
+
+inline PadWorkspace pad_workspace(const Problem& p, bool backward) {
+  PadWorkspace w{};
+  if (!padded(p)) return w;
+  const size_t nq = (size_t)p.B * p.T * p.H * p.Dk, nk = (size_t)p.B * p.T * p.Hkv * p.Dk;
+  const size_t ein = p.bf16 ? 2 : 4, eout = p.out_bf16 ? 2 : 4, edo = p.dout_bf16 ? 2 : 4;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  w.Q = take(nq * ein);
+  w.K = take(nk * ein);
+  w.V = take(nk * ein);
+  w.O = take(nq * eout);
+  if (backward) {
+    w.dO = take(nq * edo);
+    w.dQ = take(nq * 4);
+    w.dK = take(nk * 4);
+    w.dV = take(nk * 4);
+  }
+  w.inner = off;
+  return w;
+}
+
 inline FwdWorkspace fwd_workspace(const Problem& p) {
   FwdWorkspace w{};
-  size_t off = 0;
+  size_t off = pad_workspace(p, false).inner;  // padded copies first, if any
   if (ordered(p)) {
     w.chunk_lb = off;
     off = align256(off + chunk_bounds_bytes(p));
@@ -162,8 +215,9 @@ inline FwdWorkspace fwd_workspace(const Problem& p) {
   return w;
 }
 
-// Workspace layout of the backward pass (byte offsets, 256-aligned): Delta
-// and the base-2 log-sum-exp per query, per-32-query key bounds with
+// Workspace layout of the backward pass (byte offsets, 256-aligned): the
+// padded copies of a non-compiled head dim, then Delta and the base-2
+// log-sum-exp per query, per-32-query key bounds with
 // positions, a bf16 copy of an fp32 dO in fast mode, in fast mode the
 // dK/dV kernel's work counters, and the dQ and dK/dV orders when the work
 // order applies.
@@ -174,7 +228,7 @@ struct BwdWorkspace {
 inline BwdWorkspace bwd_workspace(const Problem& p) {
   BwdWorkspace w{};
   const size_t nq = (size_t)p.B * p.H * p.T;
-  size_t off = 0;
+  size_t off = pad_workspace(p, true).inner;  // padded copies first, if any
   w.delta = off;
   off = align256(off + nq * sizeof(float));
   w.lse2 = off;
@@ -182,7 +236,7 @@ inline BwdWorkspace bwd_workspace(const Problem& p) {
   w.chunk_lb = off;
   if (p.positions) off = align256(off + chunk_bounds_bytes(p));
   w.dO16 = off;
-  if (p.bf16 && !p.dout_bf16) off = align256(off + nq * p.D * sizeof(uint16_t));
+  if (p.bf16 && !p.dout_bf16) off = align256(off + nq * p.Dk * sizeof(uint16_t));
   w.queue = off;  // the fast dK/dV kernel's work counters, one per XCD
   if (p.bf16) off = align256(off + kXcds * sizeof(int32_t));
   w.qorder = off;

@@ -75,7 +75,52 @@ unsigned blocks_for(int64_t items) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Rows of src_cols values copied into rows of dst_cols values (eight per
+// thread; both counts are multiples of 16): columns past src_cols become
+// zero, columns past dst_cols are dropped; with accumulate the destination's
+// values are added in fp32 before the one rounding.  Pads a head dim to a
+// compiled width and drops the padding again (attn_api.hip).
+template <typename S, typename T>
+__global__ __launch_bounds__(kConvThreads) void repack_rows(const S* __restrict__ src, T* __restrict__ dst,
+                                                            int64_t rows, int src_cols, int dst_cols, int accumulate) {
+  const int groups = dst_cols / 8;
+  const int64_t n = rows * groups;
+  for (int64_t i = (int64_t)blockIdx.x * kConvThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kConvThreads) {
+    const int64_t row = i / groups;
+    const int c0 = 8 * (int)(i - row * groups);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = c0 < src_cols ? static_cast<float>(src[row * src_cols + c0 + e]) : 0.0f;
+    T* d = dst + row * dst_cols + c0;
+    if (accumulate) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += static_cast<float>(d[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = static_cast<T>(v[e]);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_repack(const RepackArgs& a, hipStream_t s) {
+  const int64_t items = a.rows * (a.dst_cols / 8);
+  const dim3 grid(blocks_for(items)), block(kConvThreads);
+  if (a.src_bf16 && a.dst_bf16)
+    hipLaunchKernelGGL((repack_rows<bf16_t, bf16_t>), grid, block, 0, s, static_cast<const bf16_t*>(a.src),
+                       static_cast<bf16_t*>(a.dst), a.rows, a.src_cols, a.dst_cols, a.accumulate);
+  else if (a.src_bf16)
+    hipLaunchKernelGGL((repack_rows<bf16_t, float>), grid, block, 0, s, static_cast<const bf16_t*>(a.src),
+                       static_cast<float*>(a.dst), a.rows, a.src_cols, a.dst_cols, a.accumulate);
+  else if (a.dst_bf16)
+    hipLaunchKernelGGL((repack_rows<float, bf16_t>), grid, block, 0, s, static_cast<const float*>(a.src),
+                       static_cast<bf16_t*>(a.dst), a.rows, a.src_cols, a.dst_cols, a.accumulate);
+  else
+    hipLaunchKernelGGL((repack_rows<float, float>), grid, block, 0, s, static_cast<const float*>(a.src),
+                       static_cast<float*>(a.dst), a.rows, a.src_cols, a.dst_cols, a.accumulate);
+  return hipGetLastError();
+}
+
 }  // namespace fc
 
 extern "C" {

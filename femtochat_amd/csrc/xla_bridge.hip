@@ -140,6 +140,17 @@ fc_xla_callback fc_xla_bind_attention_fwd(const fc_attn_desc* desc, int32_t has_
   // validates the descriptor on the host
   if (!report(fc_attn_workspace_bytes(desc, FC_PASS_FORWARD, has_positions != 0, &bytes), "bind attention forward"))
     return nullptr;
+  // The forward call site has no workspace buffer (its outputs are O, l, m):
+  // head dims that run zero-padded need one.
+  if (desc->D != 16 && desc->D != 32 && desc->D != 64 && desc->D != 128) {
+    char buf[256];
+    std::snprintf(buf, sizeof(buf),
+                  "bind attention forward: head_dim %d runs on padded copies in a workspace, which the XLA forward "
+                  "call site does not provide (head_dim 16, 32, 64 and 128 need none)",
+                  desc->D);
+    set_error(buf);
+    return nullptr;
+  }
   Slot s{};
   s.kind = kAttnFwd;
   s.positions = has_positions != 0;

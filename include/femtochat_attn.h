@@ -90,10 +90,13 @@ fc_status fc_attn_workspace_bytes(const fc_attn_desc* desc, int32_t pass,
    `attention!(𝒜, O, ℓ, m, Q, K, V, window)` (reference src/kernels.jl:419,
    CPU body :131-219; CUDA ext/FemtoChatCUDAExt.jl:1242-1260).
    positions may be NULL (reference semantics, no document mask).
-   The workspace is optional (NULL and 0 are accepted): in fast mode with
-   positions, a workspace of fc_attn_workspace_bytes(FC_PASS_FORWARD) bytes,
-   256-byte aligned, lets the kernel take the query tiles in order of
-   decreasing work (long documents first); the results are the same. */
+   The workspace is optional (NULL and 0 are accepted) for head_dim 16, 32,
+   64 and 128: in fast mode with positions, a workspace of
+   fc_attn_workspace_bytes(FC_PASS_FORWARD) bytes, 256-byte aligned, lets the
+   kernel take the query tiles in order of decreasing work (long documents
+   first); the results are the same.  Every other head_dim (48, 80, 96, 112)
+   runs on copies zero-padded to the next of those widths held in the
+   workspace, which is then required (FC_ERR_WORKSPACE without it). */
 fc_status fc_attn_fwd(const fc_attn_desc* desc, const void* Q, const void* K,
                       const void* V, const int32_t* positions, void* O,
                       float* l, float* m, void* workspace,
@@ -205,7 +208,10 @@ typedef struct {
 fc_status fc_capabilities(int32_t device, fc_caps* caps);
 
 /* Supported head dims are reported as a bitmask: bit (D/16 - 1) set when
-   head_dim D is compiled in. */
+   head_dim D is supported (every multiple of 16 up to 128, as the
+   reference's tensor-core path accepts, ext/FemtoChatCUDAExt.jl:214-223;
+   the kernels are compiled for 16, 32, 64 and 128 and the other widths run
+   zero-padded to the next of them). */
 uint32_t fc_attn_supported_head_dims(void);
 
 int32_t fc_abi_version(void);

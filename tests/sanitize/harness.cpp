@@ -54,7 +54,7 @@ static void validation() {
     fc_status want;
   } bad[] = {{128, 5, 2, 64, 1, FC_MODE_FAST, 0, FC_ERR_INVALID_ARGUMENT},
              {24, 4, 2, 64, 1, FC_MODE_FAST, 0, FC_ERR_INVALID_ARGUMENT},
-             {48, 4, 2, 64, 1, FC_MODE_FAST, 0, FC_ERR_UNSUPPORTED},
+             {144, 4, 2, 64, 1, FC_MODE_FAST, 0, FC_ERR_INVALID_ARGUMENT},
              {128, 4, 2, 0, 1, FC_MODE_FAST, 0, FC_ERR_INVALID_ARGUMENT},
              {128, 4, 2, 64, -3, FC_MODE_FAST, 0, FC_ERR_INVALID_ARGUMENT},
              {128, 4, 2, 64, 1, 9, 0, FC_ERR_INVALID_ARGUMENT},
@@ -70,6 +70,33 @@ static void validation() {
     CHECK(std::strlen(small) < sizeof small);
   }
   CHECK(fc::make_problem(nullptr, &p, msg, sizeof msg) == FC_ERR_INVALID_ARGUMENT);
+  // Every multiple of 16 up to 128 is accepted; the kernels run the next
+  // compiled width, and the padded copies lead both workspaces without
+  // overlapping each other or the kernels' own regions.
+  for (int D = 16; D <= 128; D += 16) {
+    for (int mode : {FC_MODE_FAST, FC_MODE_EXACT}) {
+      fc_attn_desc e = desc(D, 4, 2, 333, 3, mode);
+      CHECK(fc::make_problem(&e, &p, msg, sizeof msg) == FC_OK);
+      CHECK(p.D == D && p.Dk >= D && p.Dk - D < 64 && fc::head_dim_compiled(p.Dk));
+      CHECK(fc::padded(p) == !fc::head_dim_compiled(D));
+      const size_t el = mode == FC_MODE_FAST ? 2 : 4, nq = 3ull * 333 * 4 * p.Dk, nk = 3ull * 333 * 2 * p.Dk;
+      const fc::PadWorkspace pf = fc::pad_workspace(p, false), pb = fc::pad_workspace(p, true);
+      if (!fc::padded(p)) {
+        CHECK(pf.inner == 0 && pb.inner == 0 && fc::fwd_workspace(p).total == 0);
+        continue;
+      }
+      CHECK(pf.Q == 0 && pf.K >= nq * el && pf.V >= pf.K + nk * el && pf.O >= pf.V + nk * el &&
+            pf.inner >= pf.O + nq * el);
+      CHECK(pb.dO >= pb.O + nq * el && pb.dQ >= pb.dO + nq * el && pb.dK >= pb.dQ + nq * 4 &&
+            pb.dV >= pb.dK + nk * 4 && pb.inner >= pb.dV + nk * 4);
+      CHECK(pb.inner % 256 == 0 && pb.dQ % 256 == 0);
+      CHECK(fc::fwd_workspace(p).total == pf.inner);
+      const fc::BwdWorkspace bw = fc::bwd_workspace(p);
+      CHECK(bw.delta == pb.inner && bw.total > pb.inner);
+      const fc::Problem k = fc::kernel_problem(p, true);
+      CHECK(!k.grad_bf16 && !k.accumulate && k.D == D && k.Dk == p.Dk && fc::bwd_workspace(k).total == bw.total);
+    }
+  }
   fc_attn_desc x = desc(64, 4, 2, 100, 3, FC_MODE_EXACT);
   x.in_dtype = FC_BF16;
   CHECK(fc::make_problem(&x, &p, msg, sizeof msg) == FC_ERR_INVALID_ARGUMENT);

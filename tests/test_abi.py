@@ -49,7 +49,39 @@ def test_abi_version_and_head_dims():
     assert lib.fc_abi_version() == 1
     mask = lib.fc_attn_supported_head_dims()
     dims = [16 * (i + 1) for i in range(8) if (mask >> i) & 1]
-    assert 16 in dims and 128 in dims
+    # every multiple of 16 up to 128, as the reference's tensor-core path takes (ext/FemtoChatCUDAExt.jl:214-223)
+    assert dims == [16, 32, 48, 64, 80, 96, 112, 128]
+
+
+@pytest.mark.parametrize("D,Dk", [(48, 64), (80, 128), (96, 128), (112, 128)])
+@pytest.mark.parametrize("mode", [L.FC_MODE_FAST, L.FC_MODE_EXACT])
+def test_padded_head_dims_need_their_copies_in_the_workspace(D, Dk, mode):
+    """Head dims between the compiled widths run on zero-padded copies: the
+    forward's workspace grows by Q, K, V and O of width Dk (and becomes
+    required), the backward's by those plus dO and float32 dQ, dK, dV; a
+    compiled width asks for none of it."""
+    t = L.FC_BF16 if mode == L.FC_MODE_FAST else L.FC_F32
+    B, T, H, Hkv = 2, 64, 4, 2
+    e = 2 if t == L.FC_BF16 else 4
+    nq, nk = B * T * H * Dk, B * T * Hkv * Dk
+
+    def a256(x):
+        return (x + 255) // 256 * 256
+
+    kw = dict(D=D, H=H, Hkv=Hkv, T=T, B=B, mode=mode, in_dtype=t, out_dtype=t, dout_dtype=t, grad_dtype=t)
+    st, fwd = ws_bytes(desc(**kw), L.FC_PASS_FORWARD)
+    assert st == L.FC_OK
+    assert fwd == a256(nq * e) + 2 * a256(nk * e) + a256(nq * e)
+    st, bwd = ws_bytes(desc(**kw))
+    st_c, bwd_c = ws_bytes(desc(**dict(kw, D=Dk)))
+    assert st == st_c == L.FC_OK
+    pads = a256(nq * e) * 3 + 2 * a256(nk * e) + a256(nq * 4) + 2 * a256(nk * 4)
+    assert bwd == pads + bwd_c
+    assert ws_bytes(desc(**dict(kw, D=Dk)), L.FC_PASS_FORWARD)[1] == 0
+    # the forward of a padded head dim refuses to run without its workspace (checked before any launch)
+    fake = ctypes.c_void_p(0x1000)
+    st = L.lib().fc_attn_fwd(ctypes.byref(desc(**kw)), fake, fake, fake, None, fake, fake, fake, None, 0, None)
+    assert st == L.FC_ERR_WORKSPACE and "padded" in L.lib().fc_last_error().decode()
 
 
 def desc(**kw):
@@ -72,7 +104,6 @@ BAD = [
     (dict(H=5, Hkv=2), L.FC_ERR_INVALID_ARGUMENT, "multiple"),
     (dict(D=24), L.FC_ERR_INVALID_ARGUMENT, "head_dim"),
     (dict(D=256), L.FC_ERR_INVALID_ARGUMENT, "head_dim"),
-    (dict(D=48), L.FC_ERR_UNSUPPORTED, "not compiled"),
     (dict(T=0), L.FC_ERR_INVALID_ARGUMENT, "positive"),
     (dict(B=-1), L.FC_ERR_INVALID_ARGUMENT, "positive"),
     (dict(mode=7), L.FC_ERR_INVALID_ARGUMENT, "mode"),

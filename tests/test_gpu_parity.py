@@ -104,6 +104,50 @@ def test_small_cases(gpu, case):
     _check_case(gpu, mode, B, T, H, Hkv, D, window, seed=zlib.crc32(repr(case).encode()) % 1000)
 
 
+PADDED_CASES = [
+    # mode, B, T, H, Hkv, D, window: head dims between the compiled widths
+    ("exact", 2, 130, 4, 2, 48, (-1, 0)),
+    ("exact", 1, 100, 2, 2, 80, (16, 7)),
+    ("exact", 1, 200, 2, 1, 96, (40, 0)),
+    ("exact", 1, 77, 3, 1, 112, (-1, 0)),
+    ("fast", 2, 130, 4, 2, 48, (-1, 0)),
+    ("fast", 1, 100, 2, 2, 80, (16, 7)),
+    ("fast", 1, 200, 6, 2, 96, (40, 0)),
+    ("fast", 1, 77, 3, 1, 112, (-1, 0)),
+]
+
+
+@pytest.mark.parametrize("case", PADDED_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_padded_head_dims(gpu, case):
+    """D in {48, 80, 96, 112} (the reference's tensor-core path takes any
+    D % 16 == 0 up to 128, ext/FemtoChatCUDAExt.jl:214-223): the library runs
+    them zero-padded to 64 or 128 with the scale of the real D."""
+    mode, B, T, H, Hkv, D, window = case
+    _check_case(gpu, mode, B, T, H, Hkv, D, window, seed=zlib.crc32(repr(case).encode()) % 1000)
+
+
+def test_padded_head_dims_storage_positions_accumulate(gpu):
+    """The padded path with fp32 O/dO/gradients in fast mode, with a document
+    mask, and adding into existing bf16 gradients (the padded kernels write
+    float32 gradients that are added to the caller's values and rounded once)."""
+    pos = W.document_positions(180, 2, seed=96, mean=40, sigma=1.0, cap=120)
+    _check_case(gpu, "fast", 2, 180, 4, 2, 96, (-1, 0), positions=pos, out_dtype=torch.float32,
+                grad_dtype=torch.float32, dout_dtype=torch.float32, seed=96)
+    B, T, H, Hkv, D = 1, 150, 4, 2, 80
+    A = MFMAFast()
+    Q, K, V, dO = _inputs(9, B, T, H, Hkv, D, True)
+    Qd, Kd, Vd, dOd = (_dev(x, True, gpu) for x in (Q, K, V, dO))
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, (-1, 0))
+    base = [torch.randn(x.shape, device=gpu).to(x.dtype) for x in (Qd, Kd, Vd)]
+    fresh = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), accumulate=False, init=base)
+    added = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), accumulate=True, init=base)
+    torch.cuda.synchronize()
+    g_ref = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), (-1, 0))
+    for f, a, b0, r in zip(fresh, added, base, g_ref):
+        assert rel_err(to_np(f), r) <= TOL["fast"]
+        assert rel_err(to_np(a), to_np(f) + to_np(b0)) <= 1e-2
+
+
 @pytest.mark.parametrize("window", [(-300, 400), (-255, 300), (-701, 700)])
 def test_window_right_of_query_row_local_order(gpu, window):
     """Windows that start right of their query (left <= -255) in fast mode, with

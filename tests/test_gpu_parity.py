@@ -206,6 +206,61 @@ def test_deterministic(gpu, mode):
         assert torch.equal(x, y), "results must be bitwise reproducible"
 
 
+WS_CASES = {
+    # name: (mode, B, T, H, Hkv, D, window, positions, dO dtype) - each backward workspace layout
+    "fast_stats_in_dq": ("fast", 2, 777, 6, 3, 128, (256, 0), False, torch.bfloat16),
+    "fast_fp32_dO_positions": ("fast", 2, 500, 4, 2, 128, (-1, 0), True, torch.float32),
+    "exact_window": ("exact", 2, 300, 4, 2, 64, (100, 0), True, torch.float32),
+}
+
+
+@pytest.mark.parametrize("case", sorted(WS_CASES))
+def test_backward_ignores_prior_workspace_contents(gpu, case):
+    """The gradients depend only on the call's inputs: the same backward with
+    its workspace filled beforehand with NaN, with zeros, and with another
+    call's contents gives the same bits, and so do calls after a different
+    problem has run.  (Every workspace word a kernel reads is written earlier
+    in the same call, and every output element has one writer with a fixed
+    order of accumulation: no atomics, and the dK/dV work counters only choose
+    which workgroup runs an item.)"""
+    from femtochat_amd import backward_workspace_bytes, delta_attention_
+
+    mode, B, T, H, Hkv, D, window, with_pos, dtype = WS_CASES[case]
+    fast = mode == "fast"
+    A = MFMAFast() if fast else MFMAExact()
+    Q, K, V, dO = _inputs(23, B, T, H, Hkv, D, fast)
+    Qd, Kd, Vd = (_dev(x, fast, gpu) for x in (Q, K, V))
+    dOd = torch.from_numpy(dO).to(device=gpu, dtype=dtype)
+    pos = torch.from_numpy(W.document_positions(T, B, seed=7, mean=60, sigma=1.0, cap=300)).to(gpu) \
+        if with_pos else None
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, window, pos, out_dtype=dtype)
+    nws = backward_workspace_bytes(A, Qd, Kd, positions=pos, dout_dtype=dtype)
+    ws = torch.empty(nws, dtype=torch.uint8, device=gpu)
+    gd = dtype if fast else torch.float32
+    outs = []
+    for fill in ("nan", "zero", "previous", "other"):
+        if fill == "nan":
+            ws.view(torch.uint8).fill_(0xFF)  # every float word a NaN, every int word -1
+        elif fill == "zero":
+            ws.zero_()
+        elif fill == "other":  # a smaller, different problem through the same workspace first
+            o = [x[:1, :200].contiguous() for x in (Qd, Kd, Vd)]
+            o_dO = dOd[:1, :200].contiguous()
+            oO, ol, om = gpu_forward(A, *o, (-1, 0), out_dtype=dtype)
+            g = [torch.zeros(x.shape, dtype=gd, device=gpu) for x in o]
+            delta_attention_(A, *g, o_dO, *o, oO, ol, om, (-1, 0), accumulate=False, workspace=ws)
+        grads = [torch.full(x.shape, float("nan"), dtype=gd, device=gpu) for x in (Qd, Kd, Vd)]
+        delta_attention_(A, *grads, dOd, Qd, Kd, Vd, O, l, m, window, positions=pos, accumulate=False,
+                         workspace=ws)
+        torch.cuda.synchronize()
+        say(f"workspace {fill}: done")
+        outs.append(grads)
+    for grads in outs[1:]:
+        for name, x, y in zip(("dQ", "dK", "dV"), outs[0], grads):
+            assert not torch.isnan(y).any(), name
+            assert torch.equal(x, y), f"{name} depends on the workspace's prior contents"
+
+
 def test_cross_mix_statistics_contract(gpu):
     """Oracle forward statistics fed to the GPU backward, and GPU statistics to
     the oracle backward, agree: pins the meaning of l and m across the boundary."""

@@ -58,6 +58,12 @@ def test_binding_validates_and_returns_distinct_callbacks():
     bad = _attn_desc(H=3, Hkv=2)
     assert not lib.fc_xla_bind_attention_fwd(ctypes.byref(bad), 0)
     assert "multiple" in lib.fc_xla_last_error().decode()
+    # head_dim 96 runs on padded copies in a workspace, which the forward call site lacks;
+    # its backward call site declares the (larger) workspace and binds
+    assert not lib.fc_xla_bind_attention_fwd(ctypes.byref(_attn_desc(D=96)), 0)
+    assert "padded" in lib.fc_xla_last_error().decode()
+    n96 = ctypes.c_size_t(0)
+    assert lib.fc_xla_bind_attention_bwd(ctypes.byref(_attn_desc(D=96)), 0, ctypes.byref(n96)) and n96.value > 0
     n = ctypes.c_size_t(0)
     assert lib.fc_xla_bind_attention_bwd(ctypes.byref(_attn_desc()), 1, ctypes.byref(n))
     ref = ctypes.c_size_t(0)

@@ -474,6 +474,49 @@ def test_baseline_workload(gpu, name):
             assert eO <= tol and eL <= TOL_LSE and max(e) <= tol
 
 
+@pytest.mark.parametrize("name,layer", [("C2", 0), ("C3", 0), ("C4", 0)])
+def test_full_output_against_blocked_restatement(gpu, name, layer):
+    """Every (batch, KV group) of a full-size workload against the reference's
+    blocked algorithm restated in float32 with BLAS products
+    (oracle/fa1_blas.py, pinned to the float64 oracle in tests/test_oracle.py;
+    a few seconds on the host's BLAS threads for a whole C3 batch): O and the
+    log-sum-exp from the same inputs, and the gradients from the GPU's own O,
+    l, m on both sides, at the contract's tolerances, unit by unit."""
+    from oracle import fa1_blas
+
+    wl = W.WORKLOADS[name]
+    A = MFMAFast() if wl.mode == "fast" else MFMAExact()
+    tol = TOL[wl.mode]
+    G = wl.H // wl.Hkv
+    h = W.host_inputs(wl, layer)
+    say(f"full output {name} layer {layer} window {h.window}: B={wl.B} T={wl.T} H={wl.H} Hkv={wl.Hkv}")
+    dt = torch.bfloat16 if wl.mode == "fast" else torch.float32
+    Qd, Kd, Vd, dOd = (torch.from_numpy(x).to(gpu, dt).contiguous() for x in (h.Q, h.K, h.V, h.dO))
+    pos_d = None if h.positions is None else torch.from_numpy(h.positions).to(gpu)
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, h.window, pos_d)
+    dQ, dK, dV = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, h.window, pos_d)
+    torch.cuda.synchronize()
+    On, ln, mn = to_np(O), to_np(l), to_np(m)
+    gn = [to_np(x) for x in (dQ, dK, dV)]
+    f32 = [np.ascontiguousarray(x, dtype=np.float32) for x in (h.Q, h.K, h.V, h.dO)]
+    O_r, l_r, m_r = fa1_blas.forward(f32[0], f32[1], f32[2], h.window, h.positions)
+    g_r = fa1_blas.backward(f32[3], f32[0], f32[1], f32[2], On, ln, mn, h.window, h.positions)
+    say("  restatement done")
+    worst = [0.0] * 5
+    for b in range(wl.B):
+        for kv in range(wl.Hkv):
+            heads = slice(kv * G, (kv + 1) * G)
+            e = [rel_err(On[b, :, heads], O_r[b, :, heads]),
+                 lse_err(ln[b, heads], mn[b, heads], l_r[b, heads], m_r[b, heads]),
+                 rel_err(gn[0][b, :, heads], g_r[0][b, :, heads]),
+                 rel_err(gn[1][b, :, kv], g_r[1][b, :, kv]),
+                 rel_err(gn[2][b, :, kv], g_r[2][b, :, kv])]
+            worst = [max(w, x) for w, x in zip(worst, e)]
+    say(f"  worst over {wl.B * wl.Hkv} units: O {worst[0]:.2e} LSE {worst[1]:.2e} dQ {worst[2]:.2e} "
+        f"dK {worst[3]:.2e} dV {worst[4]:.2e}")
+    assert worst[0] <= tol and worst[1] <= TOL_LSE and max(worst[2:]) <= tol
+
+
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 

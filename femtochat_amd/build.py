@@ -15,7 +15,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
-SOURCES = ["attn_api.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_fwd_fast.hip", "attn_bwd_fast.hip", "rope_norm.hip", "loss.hip", "xla_bridge.hip", "optim.hip", "embed_sort.hip", "convert.hip"]
+SOURCES = ["attn_api.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_fwd_fast.hip", "attn_bwd_fast.hip", "attn_bwd_dkdv_vgpr.hip", "rope_norm.hip", "loss.hip", "xla_bridge.hip", "optim.hip", "embed_sort.hip", "convert.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -28,9 +28,11 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-# Per-source additions (none at present; every source builds with the flags
-# above, IEEE NaN semantics included).
-EXTRA_FLAGS = {}
+# Per-source additions.  The dK/dV kernel at head dims up to 64 selects the
+# vector-register form of every MFMA, so that S and dP are not copied out of
+# the accumulation registers element by element (at D = 128 the compiler's
+# default, accumulation-register form stays: that kernel needs both files).
+EXTRA_FLAGS = {"attn_bwd_dkdv_vgpr.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:

@@ -195,6 +195,8 @@ hipError_t launch_bwd_dq(const Problem& p, const BwdArgs& a, hipStream_t s);
 hipError_t launch_fwd_fast(const Problem& p, const FwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_dkdv_fast(const Problem& p, const BwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_dq_fast(const Problem& p, const BwdArgs& a, hipStream_t s);
+// The dK/dV kernel at head dims 16, 32 and 64 (attn_bwd_dkdv_vgpr.hip).
+hipError_t launch_bwd_dkdv_fast_vgpr(const Problem& p, const BwdArgs& a, hipStream_t s);
 
 // Profiling hooks (attn_api.hip): bracket one launch with events when enabled.
 struct ProfileMark {

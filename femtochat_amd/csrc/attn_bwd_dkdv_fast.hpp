@@ -562,6 +562,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
           }
         }
       }
+      wave_lds_sync();
 #pragma unroll
       for (int i = 0; i < 32 / RPI; ++i) {
         const int row = i * RPI + (lane + z) / U, u = (lane + z) % U;
@@ -602,6 +603,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
             for (int i = 0; i < NI; ++i) old4[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff_of(i), 0, 0);
           }
         }
+        // The previous pass's reads of the tile come before these writes, and
+        // the writes before this pass's reads (other lanes' rows).
+        wave_lds_sync();
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const int d = 32 * db + l32 + z;
@@ -613,6 +617,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_dkdv_fast_kernel(BwdArgs
             }
           }
         }
+        wave_lds_sync();
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           const int row = i * RPI + (lane + z) / U, u = (lane + z) % U;

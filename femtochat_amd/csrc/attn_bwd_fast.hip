@@ -305,6 +305,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_fast_kernel(BwdArgs a
         }
       }
     }
+    wave_lds_sync();  // the tile's rows come from other lanes
     const int q0w = q - l32;  // the wave's first query
     auto emit = [&](auto elem) __attribute__((always_inline)) {
       using E = decltype(elem);

@@ -268,4 +268,17 @@ __device__ inline void dma_wait_barrier() {
   __syncthreads();
 }
 
+// Orders the LDS accesses of one wave's lanes that exchange data through LDS
+// (an epilogue's tile, written by every lane, read back by others): the
+// writes before it are visible to the reads after it, and the reads before
+// it complete before the writes after it.  The hardware runs one wave's LDS
+// instructions in order, so no instruction is needed; without the fences the
+// compiler treats each lane's accesses as its own and may move a read past
+// other lanes' writes, or reuse an earlier read of the same address.
+__device__ __attribute__((always_inline)) inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace fc

@@ -426,6 +426,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_fast_kernel(FwdArgs a) {
         }
       }
     }
+    wave_lds_sync();  // the tile's rows come from other lanes
     constexpr int RPI = 64 / U;  // rows per store instruction
     const int q0w = qv[0] - l32;  // the wave's first query
     char* obase = static_cast<char*>(a.O) + (((int64_t)b * T * a.H + h) * D) * (int64_t)sizeof(E);

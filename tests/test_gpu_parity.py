@@ -190,6 +190,39 @@ def test_fp32_gradients_every_compiled_head_dim(gpu, D):
                 dout_dtype=torch.float32, seed=D + 1)
 
 
+@pytest.mark.parametrize("D,docs", [(16, False), (64, True), (128, False), (128, True)])
+def test_persistent_items_storage_and_accumulate(gpu, D, docs):
+    """More dK/dV items than workgroups (5 batch rows x 8 KV heads x 8 key
+    tiles = 320 items on 256 CUs), so a workgroup takes a second item while
+    its first item's gradients leave through LDS; with documents the items
+    come in the work order.  fp32 and bf16 gradients, overwritten and added
+    to the buffers' values (the fp32 sum is the same addition the caller
+    would do, so it must match bit for bit)."""
+    B, T, H, Hkv = 5, 1024, 8, 8
+    A = MFMAFast()
+    Q, K, V, dO = _inputs(D + docs, B, T, H, Hkv, D, True)
+    pos = W.document_positions(T, B, seed=D, mean=300, sigma=1.0, cap=T) if docs else None
+    pos_d = None if pos is None else torch.from_numpy(pos).to(gpu).contiguous()
+    Qd, Kd, Vd, dOd = (_dev(x, True, gpu) for x in (Q, K, V, dO))
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, (-1, 0), pos_d)
+    torch.cuda.synchronize()
+    g_ref = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), (-1, 0), pos, fast=True)
+    for gd in (torch.float32, torch.bfloat16):
+        say(f"D={D} docs={docs} grads={gd}")
+        base = [torch.randn(x.shape, device=gpu).to(gd) for x in (Qd, Kd, Vd)]
+        fresh = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), pos_d, grad_dtype=gd)
+        added = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, (-1, 0), pos_d, grad_dtype=gd, accumulate=True, init=base)
+        torch.cuda.synchronize()
+        for name, f, s, b0, r in zip(("dQ", "dK", "dV"), fresh, added, base, g_ref):
+            e = rel_err(to_np(f), r)
+            assert e <= TOL["fast"], f"{name} rel err {e}"
+            want = to_np(f) + to_np(b0)
+            if gd == torch.float32:
+                assert np.array_equal(to_np(s), want), f"{name}: accumulated fp32 differs from fresh + base"
+            else:
+                assert rel_err(to_np(s), want) <= 1e-2, f"{name}: accumulated bf16"
+
+
 @pytest.mark.parametrize("mode", ["exact", "fast"])
 def test_accumulate_and_overwrite(gpu, mode):
     fast = mode == "fast"

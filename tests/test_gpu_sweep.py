@@ -15,8 +15,11 @@ import numpy as np
 import pytest
 import torch
 
+from femtochat_amd import MFMAExact, MFMAFast
 from femtochat_amd import workloads as W
-from tests.test_gpu_parity import _check_case
+from oracle import attention_ref as R
+from tests.helpers import TOL, gpu_backward, gpu_forward, rel_err, to_np
+from tests.test_gpu_parity import _check_case, _dev, _inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -63,3 +66,39 @@ def test_sweep(gpu, case):
     f32 = torch.float32 if fp32_io else None
     _check_case(gpu, mode, B, T, H, Hkv, D, window, positions=positions, seed=seed % 1000, out_dtype=f32,
                 grad_dtype=f32, dout_dtype=f32)
+
+
+SWEEP_ACC = _draw_cases(24, seed=715)
+
+
+@pytest.mark.parametrize("case", SWEEP_ACC, ids=lambda c: "-".join(map(str, c[:9])))
+def test_sweep_accumulate(gpu, case):
+    """The same draw with the gradients added to random values already in the
+    buffers (the reference's default, Δflash_attention₁! adds into dQ, dK,
+    dV): the sum must be the overwritten result plus those values, added in
+    fp32 and rounded once (bit for bit with fp32 storage)."""
+    mode, B, T, H, Hkv, D, window, docs, fp32_io, seed = case
+    fast = mode == "fast"
+    A = MFMAFast() if fast else MFMAExact()
+    positions = None
+    if docs:
+        positions = W.document_positions(T, B, seed=seed % 100003, mean=max(4, T // 3), sigma=1.0, cap=T)
+    pos_d = None if positions is None else torch.from_numpy(positions).to(gpu).contiguous()
+    Q, K, V, dO = _inputs(seed % 1000, B, T, H, Hkv, D, fast)
+    Qd, Kd, Vd = (_dev(x, fast, gpu) for x in (Q, K, V))
+    gd = torch.float32 if (fp32_io or not fast) else torch.bfloat16
+    dOd = torch.from_numpy(dO).to(device=gpu, dtype=torch.float32 if (fp32_io or not fast) else torch.bfloat16)
+    O, l, m = gpu_forward(A, Qd, Kd, Vd, window, pos_d)
+    base = [torch.randn(x.shape, device=gpu).to(gd) for x in (Qd, Kd, Vd)]
+    fresh = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, window, pos_d, grad_dtype=gd)
+    added = gpu_backward(A, dOd, Qd, Kd, Vd, O, l, m, window, pos_d, grad_dtype=gd, accumulate=True, init=base)
+    torch.cuda.synchronize()
+    g_ref = R.backward(dO, Q, K, V, to_np(O), to_np(l), to_np(m), window, positions, fast=fast)
+    for name, f, s, b0, r in zip(("dQ", "dK", "dV"), fresh, added, base, g_ref):
+        e = rel_err(to_np(f), r)
+        assert e <= TOL[mode], f"{name} rel err {e}"
+        want = to_np(f) + to_np(b0)
+        if gd == torch.float32:
+            assert np.array_equal(to_np(s), want), f"{name}: accumulated fp32 differs from fresh + base"
+        else:
+            assert rel_err(to_np(s), want) <= 1e-2, f"{name}: accumulated bf16"

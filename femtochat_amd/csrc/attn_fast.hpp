@@ -185,22 +185,12 @@ __device__ inline u32x4s tile_words(const char* base, int64_t records, int64_t r
 }
 
 __device__ inline void dma_load16(u32x4s words, int voff, uint32_t lds_addr) {
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "buffer_load_dwordx4 %0, %1, 0 offen lds"
-      :
-      : "v"(voff), "s"(words), "s"(lds_addr)
-      : "memory", "m0");
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(words), "{m0}"(lds_addr) : "memory");
 }
 
 // The same for 4 bytes per lane (a 256-byte block of LDS).
 __device__ inline void dma_load4(u32x4s words, int voff, uint32_t lds_addr) {
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "buffer_load_dword %0, %1, 0 offen lds"
-      :
-      : "v"(voff), "s"(words), "s"(lds_addr)
-      : "memory", "m0");
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds" : : "v"(voff), "s"(words), "{m0}"(lds_addr) : "memory");
 }
 
 // Waits until at most n of this wave's global loads (LDS-DMA included) are

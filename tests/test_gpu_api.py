@@ -153,3 +153,21 @@ def test_autograd_matches_explicit_backward(gpu):
     assert torch.equal(O.detach(), st.O)
     for x, g in zip(leaves, grads):
         assert torch.equal(x.grad, g)
+
+
+def test_attention_fp16_inputs(gpu):
+    """float16 inputs select the matrix-core path as in the reference
+    (ext/FemtoChatCUDAExt.jl:214-223); this library's matrix-core format is
+    bf16, so they are converted to it (one rounding of each value, which the
+    oracle reproduces) and O comes back in float32."""
+    B, T, H, Hkv, D, window = 2, 150, 4, 2, 64, (-1, 0)
+    Q, K, V, _ = _inputs(16, B, T, H, Hkv, D)
+    Qh, Kh, Vh = (torch.from_numpy(x).half() for x in (Q, K, V))
+    assert isinstance(Kn.instruction(torch.float16, gpu, D), MFMAFast)
+    O = Kn.attention(Qh.to(gpu), Kh.to(gpu), Vh.to(gpu), window)
+    torch.cuda.synchronize()
+    assert O.dtype == torch.float32 and tuple(O.shape) == (B, T, H, D)
+    r = [x.float().bfloat16().float().numpy() for x in (Qh, Kh, Vh)]
+    O_ref, _, _ = R.forward(r[0], r[1], r[2], window)
+    e = rel_err(to_np(O), O_ref)
+    assert e <= TOL["fast"], f"O rel err {e}"

@@ -178,6 +178,16 @@ def test_fast_mode_storage_dtypes(gpu):
                 dout_dtype=torch.bfloat16)
 
 
+@pytest.mark.parametrize("mode,H,Hkv,D", [("fast", 32, 1, 64), ("fast", 16, 2, 128), ("exact", 24, 3, 32),
+                                          ("fast", 12, 12, 16)])
+def test_wide_gqa_groups(gpu, mode, H, Hkv, D):
+    """GQA groups of 1 to 32 query heads per KV head: the dK/dV kernels sum the
+    group's heads in registers (one item loops over all of them), and the
+    forward and dQ map every query head to its KV head."""
+    _check_case(gpu, mode, 2, 160, H, Hkv, D, (-1, 0), seed=H * 7 + Hkv)
+    _check_case(gpu, mode, 1, 97, H, Hkv, D, (40, 3), seed=H * 7 + Hkv + 1)
+
+
 @pytest.mark.parametrize("D", [16, 32, 64, 128])
 def test_fp32_gradients_every_compiled_head_dim(gpu, D):
     """fp32 dQ, dK, dV at every compiled head dim.  The epilogues stage the
